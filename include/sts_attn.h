@@ -1,0 +1,273 @@
+/*
+ * sts_attn.h -- C ABI of the MI355X (gfx950) attention hot path of sts-web.
+ *
+ * This library replaces, behind plain C entry points, the attention op and the
+ * ring-buffer KV cache of idle-intelligence/sts-web (paths below are relative
+ * to crates/sts-wasm/src/ of that repository):
+ *
+ *   fused_attention          model.rs:598-668  + wgsl/shader_attention.wgsl
+ *   gpu_cache_write_v        model.rs:143-188  + wgsl/shader_cache_write.wgsl
+ *   KVCache / LayerCaches    model.rs:195-411
+ *   RoPE                     model.rs:38-122
+ *   prefill branch           model.rs:760-797, 837-873 (causal mask 539-563)
+ *   depformer step attention depth.rs:79-273, depth_engine.rs:1121-1209
+ *
+ * Conventions (every entry point):
+ *   - Returns int status: STS_OK (0) on success, a negative STS_ERR_* code
+ *     otherwise.  sts_last_error() returns a message for the calling thread's
+ *     last failure.  No entry point aborts the process.
+ *   - Pointers named q/k/v/out/input/cache are DEVICE pointers (hipMalloc'd or
+ *     owned by the caller's tensor library), f32, contiguous as documented.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
+ *     device work is enqueued asynchronously on it; nothing blocks the host
+ *     except the one-time allocation of library workspace (see below).
+ *   - head_dim must be 64 or 128 (the two head sizes of the model: temporal
+ *     4096/32, depformer 1024/16; lib.rs:128-140).  The reference shader
+ *     silently overflows for head_dim > 128 (shader_attention.wgsl:66); here it
+ *     is an error.
+ *   - Attention entry points use a per-(device, stream) workspace owned by the
+ *     library for split-KV partial results.  It is allocated (hipMalloc) on the
+ *     first call on a stream and grown when a larger launch needs it; warm a
+ *     stream up before capturing it in a HIP graph.  Calls issued on the same
+ *     stream are ordered; calls on different streams use different workspaces.
+ *   - Handles are not internally locked: use one handle from one host thread at
+ *     a time (the reference's caches are !Sync, model.rs:483).
+ */
+#ifndef STS_ATTN_H
+#define STS_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STS_ATTN_ABI_VERSION 1
+
+enum sts_status {
+  STS_OK = 0,
+  STS_ERR_INVALID = -1, /* bad argument: null pointer, size, head_dim, range */
+  STS_ERR_HIP = -2,     /* a HIP runtime call failed (message has the code)  */
+  STS_ERR_STATE = -3,   /* handle in the wrong state for the call            */
+  STS_ERR_NOMEM = -4    /* device or host allocation failed                  */
+};
+
+enum sts_precision {
+  STS_PREC_F32 = 0,      /* f32 inputs, f32 arithmetic                       */
+  STS_PREC_BF16_MFMA = 1 /* f32 inputs rounded to bf16 for MFMA, f32 accumulate */
+};
+
+/* Message for the calling thread's most recent failed call ("" if none). */
+const char* sts_last_error(void);
+
+/* STS_ATTN_ABI_VERSION of the loaded library. */
+int sts_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Stateless ops (raw device pointers)                                       */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Single-query attention over the first `seq_len` rows of a K/V buffer.
+ * Replaces fused_attention (model.rs:598-668), which launches
+ * shader_attention.wgsl with info [num_heads, head_dim, seq_len, scale_bits,
+ * kv_head_stride] (model.rs:631-640).
+ *   q   [num_heads][head_dim]                        (contiguous)
+ *   k,v row p of head h at  h*kv_head_stride + p*head_dim   (p < seq_len)
+ *   out [num_heads][head_dim]                        (caller-owned)
+ *   out_h = sum_p softmax_p(scale * q_h . k_{h,p}) v_{h,p}
+ * seq_len must be >= 1 and kv_head_stride >= seq_len*head_dim.
+ */
+int sts_fused_attention(const float* q, const float* k, const float* v, float* out,
+                        uint32_t num_heads, uint32_t head_dim, uint32_t seq_len,
+                        float scale, uint64_t kv_head_stride, void* stream);
+
+/*
+ * Ring-buffer append.  Replaces gpu_cache_write_v (model.rs:143-188) and
+ * shader_cache_write.wgsl:19-49, bit for bit:
+ *   cache[((b*H + h)*max_len + (pos_offset + s) % max_len)*D + d]
+ *       = input[((b*S + s)*H + h)*D + d]
+ *   input [B][S][H][D],  cache [B][H][max_len][D].
+ * Any head_dim >= 1 is accepted here (pure copy).  Slots not addressed are
+ * left untouched.  Writes from one call must not collide: S <= max_len.
+ */
+int sts_cache_write(const float* input, float* cache, uint32_t pos_offset,
+                    uint32_t batch, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                    uint32_t max_len, void* stream);
+
+/*
+ * Decode attention over a wrapped ring window, batched over streams with
+ * ragged lengths (the generalisation of fused_attention that the cache needs
+ * once the ring wraps; the reference's view assumes the window starts at slot
+ * 0, model.rs:252-258).
+ *   q, out       [batch][heads][head_dim]
+ *   k/v cache    [batch][heads][max_len][head_dim]
+ *   lens[b]      valid rows of stream b, 0..max_len   (device int32 array)
+ *   starts[b]    slot of stream b's oldest row, 0..max_len-1 (device int32)
+ *   row i (0 <= i < lens[b]) of stream b lives in slot (starts[b]+i) % max_len
+ * A stream with lens[b] == 0 gets out = 0.  lens/starts outside their ranges
+ * are clamped on the device (len to max_len, start modulo max_len).
+ */
+int sts_decode_ring(const float* q, const float* k_cache, const float* v_cache,
+                    float* out, const int32_t* lens, const int32_t* starts,
+                    uint32_t batch, uint32_t heads, uint32_t head_dim, uint32_t max_len,
+                    float scale, void* stream);
+
+/*
+ * Depformer step attention, batched over independent streams: appends the
+ * step's K/V row at slot `step` and attends over slots 0..step (L = step+1),
+ * in one launch.  Replaces the per-step cache-write K, cache-write V and
+ * attention dispatches of depth_engine.rs:1121-1209 (info buffers
+ * depth_engine.rs:626-645, 725-741) and the decode branch of
+ * MultiLinearAttention (depth.rs:104-119, 203-217).
+ *   q, k_new, v_new: stream b's rows at  ptr + b*qkv_stride  ([heads][head_dim]
+ *                    each; qkv_stride = 3*heads*head_dim for a packed qkv_out)
+ *   k/v cache        [batch][heads][max_len][head_dim]
+ *   out              [batch][heads][head_dim]
+ * Requires step < max_len.  No RoPE (depformer has none, depth.rs:100).
+ */
+int sts_depformer_step(const float* q, const float* k_new, const float* v_new,
+                       uint64_t qkv_stride, float* k_cache, float* v_cache, float* out,
+                       uint32_t batch, uint32_t heads, uint32_t head_dim,
+                       uint32_t max_len, uint32_t step, float scale, void* stream);
+
+/*
+ * Chunked causal prefill attention over a ring window (batch 1).  The chunk's
+ * `seq` rows must already be appended: they are the last `seq` rows of the
+ * window.  Query i (0 <= i < seq) sits at window row w_i = win_len - seq + i
+ * and attends window rows 0..w_i.  This is the semantics of the reference's
+ * prefill branch (model.rs:784-792, mask model.rs:551-557: key j masked when
+ * j > offset + i) and of the S sequential decodes the reference actually runs
+ * (stream.rs:482-492).
+ *   q, out     [seq][heads][head_dim]
+ *   k/v cache  [heads][max_len][head_dim];  window row r in slot (win_start + r) % max_len
+ * precision: STS_PREC_F32 or STS_PREC_BF16_MFMA.
+ */
+int sts_prefill_attention(const float* q, const float* k_cache, const float* v_cache,
+                          float* out, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                          uint32_t max_len, uint32_t win_start, uint32_t win_len,
+                          float scale, int precision, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* RoPE (model.rs:38-122)                                                     */
+/* ------------------------------------------------------------------------ */
+
+typedef struct sts_rope sts_rope;
+
+/*
+ * Builds the cos/sin tables [max_seq_len][head_dim/2] of RoPE::new
+ * (model.rs:46-66): inv_freq_j = 1 / theta^(2j/head_dim) and
+ * angle = pos * inv_freq_j, both in f32 as the reference computes them; cos
+ * and sin of each f32 angle are rounded to nearest f32.  Uploads them to the
+ * current device (synchronous, once).
+ */
+int sts_rope_create(uint32_t head_dim, uint32_t max_seq_len, float theta, sts_rope** out);
+int sts_rope_destroy(sts_rope* rope);
+
+/*
+ * In-place interleaved rotation of x [batch][seq][heads][head_dim] at
+ * positions offset..offset+seq-1 (RoPE::apply_rope_to_tensor,
+ * model.rs:79-105): pair (x0, x1) = (x[2j], x[2j+1]) becomes
+ * (x0*c - x1*s, x0*s + x1*c).  offset+seq must not exceed max_seq_len
+ * (the reference slices the table there, model.rs:92-95).
+ */
+int sts_rope_apply(const sts_rope* rope, float* x, uint32_t batch, uint32_t seq,
+                   uint32_t heads, uint32_t offset, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* KV cache handle (KVCache, model.rs:195-363)                               */
+/* ------------------------------------------------------------------------ */
+
+typedef struct sts_kv_cache sts_kv_cache;
+
+typedef struct sts_kv_state {
+  uint64_t offset;    /* logical rows ever appended, minus rollbacks       */
+  uint64_t len;       /* valid rows, min(count, max_len)                   */
+  uint64_t write_pos; /* next slot to write, offset % max_len unless rolled */
+  uint64_t max_len;
+  uint64_t heads;
+  uint64_t head_dim;
+  uint64_t batch;     /* 0 until the buffers are allocated                 */
+  int32_t allocated;  /* 1 when the K/V buffers exist                      */
+  int32_t reserved;
+} sts_kv_state;
+
+/* KVCache::new (model.rs:207-219).  Allocates nothing on the device. */
+int sts_kv_create(uint64_t max_len, uint64_t heads, uint64_t head_dim, sts_kv_cache** out);
+int sts_kv_destroy(sts_kv_cache* cache);
+
+/*
+ * KVCache::ensure_allocated (model.rs:270-284): allocates zero-filled K and V
+ * buffers [batch][heads][max_len][head_dim] on first use and returns them with
+ * the current write position.  A later call with another batch fails.
+ */
+int sts_kv_ensure_allocated(sts_kv_cache* cache, uint64_t batch, float** k, float** v,
+                            uint64_t* write_pos, void* stream);
+
+/* Counters (model.rs:313-323), plus write_pos and allocation state. */
+int sts_kv_get_state(const sts_kv_cache* cache, sts_kv_state* out);
+
+/*
+ * The logical window: row i (0 <= i < len) is in slot (start + i) % max_len,
+ * start = (write_pos + max_len - len) % max_len.
+ */
+int sts_kv_window(const sts_kv_cache* cache, uint64_t* start, uint64_t* len);
+
+/* KVCache::advance (model.rs:293-311), counters only. */
+int sts_kv_advance(sts_kv_cache* cache, uint64_t n);
+
+/*
+ * Append `seq` rows and advance: KVCache::update (model.rs:221-268), with the
+ * chunk written at slots (offset+s) % max_len as gpu_cache_write_v does (the
+ * reference's update writes a single slot, model.rs:245-246).  k_new, v_new
+ * are [batch][seq][heads][head_dim].  Allocates on first use.  seq <= max_len.
+ */
+int sts_kv_update(sts_kv_cache* cache, const float* k_new, const float* v_new,
+                  uint64_t batch, uint64_t seq, void* stream);
+
+/* KVCache::reset (model.rs:325-331): frees the buffers, zeroes counters. */
+int sts_kv_reset(sts_kv_cache* cache);
+
+/* KVCache::reset_keep_buffers (model.rs:333-345): zero-fills, zeroes counters. */
+int sts_kv_reset_keep_buffers(sts_kv_cache* cache, void* stream);
+
+/* KVCache::rollback (model.rs:352-362): n is clamped to len. */
+int sts_kv_rollback(sts_kv_cache* cache, uint64_t n);
+
+/*
+ * Decode attention over the cache's current window for each stream of the
+ * batch (equal lengths): q, out [batch][heads][head_dim].  This is
+ * fused_attention(q, k_all, v_all) on the views advance() returns
+ * (model.rs:829-831), generalised to a wrapped window.
+ */
+int sts_kv_attend(sts_kv_cache* cache, const float* q, float* out, float scale, void* stream);
+
+/*
+ * One fused decode step of the temporal (or depformer) attention: optional
+ * RoPE of q and k_new at position `offset`, append of k_new/v_new at slot
+ * write_pos, advance(1), and attention over the new window -- the decode
+ * branch of Q4Attention::forward_with_cache (model.rs:739-758, 818-835) in one
+ * launch.  q, k_new, v_new, out are [batch][heads][head_dim].  `rope` may be
+ * NULL (depformer, depth.rs:100); when given, q and k_new are read unrotated
+ * and the rotated q is not written back.  Allocates the cache on first use.
+ */
+int sts_kv_decode_step(sts_kv_cache* cache, const sts_rope* rope, const float* q,
+                       const float* k_new, const float* v_new, float* out,
+                       uint64_t batch, float scale, void* stream);
+
+/*
+ * Chunked prefill (batch 1): append `seq` rows of k_new/v_new
+ * ([seq][heads][head_dim], RoPE already applied) and run causal attention of
+ * the `seq` queries q [seq][heads][head_dim] over the grown window into out.
+ * The prefill branch of model.rs:760-797 with a working multi-row append.
+ */
+int sts_kv_prefill(sts_kv_cache* cache, const float* q, const float* k_new,
+                   const float* v_new, float* out, uint64_t seq, float scale,
+                   int precision, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STS_ATTN_H */

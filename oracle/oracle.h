@@ -1,0 +1,123 @@
+/*
+ * oracle.h -- CPU restatement of sts-web's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this code, and only as the checker or
+ * as the timed CPU baseline -- never as a product path.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * crates/sts-wasm/src/ of idle-intelligence/sts-web).  How each one is pinned
+ * (closed forms, library routines, reference unit tests) is listed in
+ * oracle/README.md.
+ */
+#ifndef STS_ORACLE_H
+#define STS_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- test-data RNG (our spec; no reference counterpart) ------------------ */
+
+/* SplitMix64 output for counter i:  mix(seed + (i+1) * 0x9E3779B97F4A7C15). */
+uint64_t orc_splitmix64(uint64_t seed, uint64_t i);
+
+/*
+ * out[j] = N(0,1) sample number (first + j) of stream `seed`, by Box-Muller on
+ * SplitMix64 counters: pair k uses counters 2k and 2k+1,
+ *   u1 = ((c0 >> 40) + 1) * 2^-24,  u2 = (c1 >> 40) * 2^-24,
+ *   r = sqrt(-2 ln u1),  sample 2k = r cos(2 pi u2),  2k+1 = r sin(2 pi u2),
+ * evaluated in double and rounded to f32.  OpenMP-parallel.
+ */
+void orc_fill_normal(uint64_t seed, uint64_t first, uint64_t n, float* out);
+
+/* ---- RoPE (model.rs:38-122) ---------------------------------------------- */
+
+/* RoPE::new tables (model.rs:46-66): cos_t, sin_t [max_seq_len][head_dim/2]. */
+void orc_rope_tables(uint32_t head_dim, uint32_t max_seq_len, float theta,
+                     float* cos_t, float* sin_t);
+
+/* RoPE::apply_rope_to_tensor (model.rs:79-105), in place on x [B][S][H][D]. */
+void orc_rope_apply(float* x, uint32_t B, uint32_t S, uint32_t H, uint32_t D,
+                    uint32_t offset, const float* cos_t, const float* sin_t);
+
+/* ---- KV append (shader_cache_write.wgsl:19-49, model.rs:143-188) -------- */
+
+void orc_cache_write(const float* input, float* cache, uint32_t pos_offset,
+                     uint32_t B, uint32_t S, uint32_t H, uint32_t D, uint32_t max_len);
+
+/* ---- KV cache counters (model.rs:195-363) -------------------------------- */
+
+typedef struct orc_kv {
+  uint64_t offset, len, write_pos, max_len;
+} orc_kv;
+
+void orc_kv_init(orc_kv* c, uint64_t max_len);       /* KVCache::new      */
+void orc_kv_advance(orc_kv* c, uint64_t n);          /* advance  :293-302 */
+void orc_kv_update(orc_kv* c);                       /* update   :245-251 */
+void orc_kv_reset(orc_kv* c);                        /* reset    :325-331 */
+void orc_kv_rollback(orc_kv* c, uint64_t n);         /* rollback :352-362 */
+
+/* ---- decode attention ---------------------------------------------------- */
+
+/*
+ * shader_attention.wgsl:43-156 in its exact f32 evaluation order: 256 lanes,
+ * lane t takes rows t, t+256, ...; per-lane online softmax; tree merge of
+ * (max, sum); per-dimension tree sum; divide by the sum.  One "workgroup" per
+ * head; OpenMP over heads.  q/out [H][D]; k/v row p of head h at
+ * h*kv_head_stride + p*D.
+ */
+void orc_attention_wgsl(const float* q, const float* k, const float* v, float* out,
+                        uint32_t H, uint32_t D, uint32_t S, float scale,
+                        uint64_t kv_head_stride);
+
+/*
+ * The same, over a wrapped ring window: row i of head h is slot
+ * (start + i) % M of a [H][M][D] cache.  The window is gathered into order
+ * and passed to orc_attention_wgsl (the reference's view is the unwrapped
+ * special case start = 0, model.rs:252-258).
+ */
+void orc_attention_ring_wgsl(const float* q, const float* kc, const float* vc, float* out,
+                             uint32_t H, uint32_t D, uint32_t M, uint32_t start,
+                             uint32_t len, float scale);
+
+/*
+ * Textbook softmax(scale * q K^T) V in double over the same ring window
+ * (the closed form the shader computes).  out is double [H][D].
+ */
+void orc_attention_ring_f64(const float* q, const float* kc, const float* vc, double* out,
+                            uint32_t H, uint32_t D, uint32_t M, uint32_t start,
+                            uint32_t len, double scale);
+
+/* ---- chunked prefill ----------------------------------------------------- */
+
+/*
+ * Causal prefill in double: q/out [S][H][D]; query i sits at window row
+ * w_i = len - S + i and attends window rows 0..w_i (model.rs:551-557 mask
+ * "j > offset + i", applied to softmax((Q K^T) * scale) V, model.rs:789-792).
+ */
+void orc_prefill_f64(const float* q, const float* kc, const float* vc, double* out,
+                     uint32_t S, uint32_t H, uint32_t D, uint32_t M, uint32_t start,
+                     uint32_t len, double scale);
+
+/*
+ * What the reference actually executes for a prefill (stream.rs:482-492):
+ * S sequential decodes, query i over the first w_i + 1 window rows, each in
+ * the shader's f32 order.  q/out [S][H][D].
+ */
+void orc_prefill_seq_wgsl(const float* q, const float* kc, const float* vc, float* out,
+                          uint32_t S, uint32_t H, uint32_t D, uint32_t M, uint32_t start,
+                          uint32_t len, float scale);
+
+/* Number of OpenMP threads the oracle uses (for the CPU-baseline record). */
+int orc_num_threads(void);
+void orc_set_num_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,112 @@
+// append.hip -- ring-buffer KV append and RoPE for gfx950.
+//
+// cache_write replaces shader_cache_write.wgsl (crates/sts-wasm/src/wgsl/
+// shader_cache_write.wgsl:19-49): the same slot formula, moved as 128-bit
+// vectors when head_dim allows (bit-identical, it is a copy).  rope_apply
+// replaces RoPE::apply_rope_to_tensor (crates/sts-wasm/src/model.rs:79-105).
+#include "append.hpp"
+#include "common.hpp"
+
+namespace sts {
+
+namespace {
+
+// One thread per 4 consecutive elements of input [B][S][H][D] (D % 4 == 0).
+__global__ __launch_bounds__(256) void cache_write_vec4(const float4* __restrict__ in,
+                                                        float* __restrict__ cache,
+                                                        uint32_t pos_offset, uint32_t S,
+                                                        uint32_t H, uint32_t D4,
+                                                        uint32_t max_len, uint64_t total4) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total4) return;
+  const uint32_t d4 = (uint32_t)(i % D4);
+  const uint64_t rem = i / D4;
+  const uint32_t h = (uint32_t)(rem % H);
+  const uint64_t rem2 = rem / H;
+  const uint32_t s = (uint32_t)(rem2 % S);
+  const uint64_t b = rem2 / S;
+  const uint32_t slot = (uint32_t)(((uint64_t)pos_offset + s) % max_len);
+  const uint64_t dst = ((b * H + h) * max_len + slot) * D4 + d4;
+  reinterpret_cast<float4*>(cache)[dst] = in[i];
+}
+
+// Scalar form for head_dim not a multiple of 4 (the shader's own shape).
+__global__ __launch_bounds__(256) void cache_write_scalar(const float* __restrict__ in,
+                                                          float* __restrict__ cache,
+                                                          uint32_t pos_offset, uint32_t S,
+                                                          uint32_t H, uint32_t D,
+                                                          uint32_t max_len, uint64_t total) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t d = (uint32_t)(i % D);
+  const uint64_t rem = i / D;
+  const uint32_t h = (uint32_t)(rem % H);
+  const uint64_t rem2 = rem / H;
+  const uint32_t s = (uint32_t)(rem2 % S);
+  const uint64_t b = rem2 / S;
+  const uint32_t slot = (uint32_t)(((uint64_t)pos_offset + s) % max_len);
+  cache[((b * H + h) * max_len + slot) * D + d] = in[i];
+}
+
+// One thread per two adjacent rotation pairs (4 floats) of x [B][S][H][D].
+__global__ __launch_bounds__(256) void rope_kernel(float4* __restrict__ x,
+                                                   const float2* __restrict__ cos_t,
+                                                   const float2* __restrict__ sin_t,
+                                                   uint32_t S, uint32_t H, uint32_t D4,
+                                                   uint32_t offset, uint64_t total4) {
+#pragma clang fp contract(off)
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total4) return;
+  const uint32_t d4 = (uint32_t)(i % D4);
+  const uint32_t s = (uint32_t)((i / D4 / H) % S);
+  // A table row holds D/2 floats; float2 entry d4 covers pairs 2*d4, 2*d4+1.
+  const uint64_t row = (uint64_t)(offset + s) * D4 + d4;
+  const float2 c = cos_t[row];
+  const float2 sn = sin_t[row];
+  const float4 v = x[i];
+  float4 y;
+  y.x = v.x * c.x - v.y * sn.x;
+  y.y = v.x * sn.x + v.y * c.x;
+  y.z = v.z * c.y - v.w * sn.y;
+  y.w = v.z * sn.y + v.w * c.y;
+  x[i] = y;
+}
+
+}  // namespace
+
+int launch_cache_write(const float* input, float* cache, uint32_t pos_offset, uint32_t batch,
+                       uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_len,
+                       hipStream_t stream) {
+  const uint64_t total = (uint64_t)batch * seq * heads * head_dim;
+  if (total == 0) return STS_OK;
+  const bool vec = (head_dim % 4 == 0) && ((uintptr_t)input % 16 == 0) &&
+                   ((uintptr_t)cache % 16 == 0);
+  if (vec) {
+    const uint64_t total4 = total / 4;
+    const uint64_t blocks = (total4 + 255) / 256;
+    hipLaunchKernelGGL(cache_write_vec4, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(input), cache, pos_offset, seq, heads,
+                       head_dim / 4, max_len, total4);
+  } else {
+    const uint64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(cache_write_scalar, dim3((uint32_t)blocks), dim3(256), 0, stream, input,
+                       cache, pos_offset, seq, heads, head_dim, max_len, total);
+  }
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+int launch_rope(float* x, const float* cos_t, const float* sin_t, uint32_t batch, uint32_t seq,
+                uint32_t heads, uint32_t head_dim, uint32_t offset, hipStream_t stream) {
+  const uint64_t total4 = (uint64_t)batch * seq * heads * head_dim / 4;
+  if (total4 == 0) return STS_OK;
+  const uint64_t blocks = (total4 + 255) / 256;
+  hipLaunchKernelGGL(rope_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<float4*>(x), reinterpret_cast<const float2*>(cos_t),
+                     reinterpret_cast<const float2*>(sin_t), seq, heads, head_dim / 4, offset,
+                     total4);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+}  // namespace sts

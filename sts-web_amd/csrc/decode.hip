@@ -1,0 +1,395 @@
+// decode.hip -- split-KV decode attention for gfx950.
+//
+// Replaces shader_attention.wgsl (crates/sts-wasm/src/wgsl/shader_attention.wgsl:43-156),
+// which runs one 256-lane workgroup per head, each lane streaming whole
+// 512-byte rows.  Here the window of every (stream, head) is cut into splits
+// of `chunk` rows; each workgroup streams one split with 128-bit loads that
+// are contiguous across lanes, keeps an online softmax per row group, merges
+// its waves through LDS, and the last workgroup of a (stream, head) to finish
+// merges the splits (log-sum-exp) and writes the output.
+//
+// Layout per wave (D = head_dim, G = D/4 lanes per row, NG = 64/G row groups):
+//   lane = g*G + c holds dims [4c, 4c+4) of the rows of group g; one loop
+//   iteration covers RPI = NG * (G/4) = 16 rows, row r0 + j*NG + g for j < G/4.
+// Dot products are reduced over the G lanes of a group with a transposing
+// butterfly (DPP + ds_swizzle), which leaves lane c holding the score of row
+// j = (c >> 2) & (G/4 - 1), replicated over a quad.
+//
+// Softmax uses exp(x) = 2^(x log2 e): q is pre-multiplied by scale*log2(e) and
+// the hardware base-2 exponential is applied to (s - m) <= 0.
+#include <cfloat>
+
+#include "common.hpp"
+#include "decode.hpp"
+#include "lane.hpp"
+
+namespace sts {
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// Interleaved RoPE of two adjacent pairs (model.rs:99-100), each product and
+// sum rounded separately as the reference evaluates them.
+__device__ __forceinline__ float4 rope4(float4 x, float2 cs, float2 sn) {
+#pragma clang fp contract(off)
+  float4 y;
+  y.x = x.x * cs.x - x.y * sn.x;
+  y.y = x.x * sn.x + x.y * cs.x;
+  y.z = x.z * cs.y - x.w * sn.y;
+  y.w = x.z * sn.y + x.w * cs.y;
+  return y;
+}
+
+// One transposing butterfly level: N values in, N/2 out.  The lane whose bit
+// LEVEL is set keeps the upper half, its partner the lower half.
+template <int LEVEL, int N>
+__device__ __forceinline__ void transpose_level(float* s, int c) {
+  const bool hi = (c >> LEVEL) & 1;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float lo_v = s[i], hi_v = s[i + N / 2];
+    const float send = hi ? lo_v : hi_v;
+    const float keep = hi ? hi_v : lo_v;
+    s[i] = keep + xchg<LEVEL>(send);
+  }
+}
+
+// Sums RPG = G/4 per-lane partial dots over the G lanes of a row group; lane c
+// ends with row (c >> 2) & (RPG-1).
+template <int G>
+__device__ __forceinline__ float reduce_rows(float* s, int c) {
+  if constexpr (G == 32) {
+    transpose_level<4, 8>(s, c);
+    transpose_level<3, 4>(s, c);
+    transpose_level<2, 2>(s, c);
+  } else {
+    static_assert(G == 16, "head_dim 64 or 128");
+    transpose_level<3, 4>(s, c);
+    transpose_level<2, 2>(s, c);
+  }
+  float x = s[0];
+  x += xchg<1>(x);
+  x += xchg<0>(x);
+  return x;
+}
+
+// Max over the RPG distinct rows of a group (quads hold replicas).
+template <int G>
+__device__ __forceinline__ float group_max(float x) {
+  x = fmaxf(x, xchg<2>(x));
+  x = fmaxf(x, xchg<3>(x));
+  if constexpr (G == 32) x = fmaxf(x, xchg<4>(x));
+  return x;
+}
+
+// Sum over all 64 lanes.
+__device__ __forceinline__ float wave_sum(float x) {
+  x += xchg<0>(x);
+  x += xchg<1>(x);
+  x += xchg<2>(x);
+  x += xchg<3>(x);
+  x += xchg<4>(x);
+  x += xor32(x);
+  return x;
+}
+
+template <int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p) {
+  constexpr int G = D / 4;
+  constexpr int NG = 64 / G;
+  constexpr int RPG = G / 4;
+  constexpr int RPI = NG * RPG;
+  static_assert(RPI == 16, "16 rows per wave iteration");
+
+  __shared__ __align__(16) float s_p[WAVES][RPI];
+  __shared__ __align__(16) float s_acc[WAVES][D];
+  __shared__ float s_ml[WAVES][2];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane / G;
+  const int c = lane % G;
+  const uint32_t split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+
+  uint32_t len, start;
+  if (p.lens) {
+    const int32_t L = p.lens[b];
+    len = L <= 0 ? 0u : min((uint32_t)L, p.M);
+    const int32_t st = p.starts[b] % (int32_t)p.M;
+    start = (uint32_t)(st < 0 ? st + (int32_t)p.M : st);
+  } else {
+    len = p.len;
+    start = p.start;
+  }
+
+  float* outp = p.out + b * p.out_bstride + (size_t)h * D;
+  if (len == 0) {
+    if (split == 0)
+      for (int t = tid; t < D; t += WAVES * 64) outp[t] = 0.f;
+    return;
+  }
+  const uint32_t i0 = split * p.chunk;
+  if (i0 >= len) return;
+  const uint32_t i1 = min(len, i0 + p.chunk);
+  const uint32_t nsplit = (len + p.chunk - 1) / p.chunk;
+
+  const size_t qoff = b * p.q_bstride + (size_t)h * D + c * 4;
+  float4 q4 = ld4(p.q + qoff);
+  float2 rc = make_float2(0.f, 0.f), rs = make_float2(0.f, 0.f);
+  const bool rope = p.rope_cos != nullptr;
+  if (rope) {
+    const size_t ro = (size_t)p.rope_pos * (D / 2) + c * 2;
+    rc = *reinterpret_cast<const float2*>(p.rope_cos + ro);
+    rs = *reinterpret_cast<const float2*>(p.rope_sin + ro);
+    q4 = rope4(q4, rc, rs);
+  }
+  q4.x *= p.scale_log2;
+  q4.y *= p.scale_log2;
+  q4.z *= p.scale_log2;
+  q4.w *= p.scale_log2;
+
+  const size_t kvoff = b * p.kv_bstride + h * p.kv_hstride;
+  const float* kh = p.k + kvoff + c * 4;
+  const float* vh = p.v + kvoff + c * 4;
+  const bool append = p.k_new != nullptr;
+  const uint32_t new_row = len - 1;
+
+  float m = -FLT_MAX;
+  float lsum = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int jj = (c >> 2) & (RPG - 1);
+
+  for (uint32_t r0 = i0 + wave * RPI; r0 < i1; r0 += WAVES * RPI) {
+    float4 kk[RPG], vv[RPG];
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      const uint32_t r = r0 + j * NG + g;
+      uint32_t slot = start + r;
+      slot = slot >= p.M ? slot - p.M : slot;
+      if (r < i1) {
+        if (append && r == new_row) {
+          float4 kn = ld4(p.k_new + qoff);
+          const float4 vn = ld4(p.v_new + qoff);
+          if (rope) kn = rope4(kn, rc, rs);
+          st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
+          st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
+          kk[j] = kn;
+          vv[j] = vn;
+        } else {
+          kk[j] = ld4(kh + (size_t)slot * D);
+          vv[j] = ld4(vh + (size_t)slot * D);
+        }
+      } else {
+        kk[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        vv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float s[RPG];
+#pragma unroll
+    for (int j = 0; j < RPG; ++j)
+      s[j] = q4.x * kk[j].x + q4.y * kk[j].y + q4.z * kk[j].z + q4.w * kk[j].w;
+    float sc = reduce_rows<G>(s, c);
+    const uint32_t my_row = r0 + jj * NG + g;
+    sc = my_row < i1 ? sc : -INFINITY;
+    const float mn = fmaxf(m, group_max<G>(sc));
+    const float alpha = fast_exp2(m - mn);
+    const float pj = fast_exp2(sc - mn);
+    m = mn;
+    lsum = lsum * alpha + pj;
+    if ((c & 3) == 0) s_p[wave][g * RPG + jj] = pj;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float pp[RPG];
+#pragma unroll
+    for (int j = 0; j < RPG; j += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(&s_p[wave][g * RPG + j]);
+      pp[j] = t.x;
+      pp[j + 1] = t.y;
+      pp[j + 2] = t.z;
+      pp[j + 3] = t.w;
+    }
+    acc.x *= alpha;
+    acc.y *= alpha;
+    acc.z *= alpha;
+    acc.w *= alpha;
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      acc.x += pp[j] * vv[j].x;
+      acc.y += pp[j] * vv[j].y;
+      acc.z += pp[j] * vv[j].z;
+      acc.w += pp[j] * vv[j].w;
+    }
+  }
+
+  // Merge the NG row groups of the wave (lanes c, c+G, ... hold the same dims).
+  float mw = m;
+  if constexpr (NG == 4) mw = fmaxf(mw, xchg<4>(mw));
+  mw = fmaxf(mw, xor32(mw));
+  {
+    const float f = fast_exp2(m - mw);
+    acc.x *= f;
+    acc.y *= f;
+    acc.z *= f;
+    acc.w *= f;
+    lsum *= f;
+  }
+  if constexpr (NG == 4) {
+    acc.x += xchg<4>(acc.x);
+    acc.y += xchg<4>(acc.y);
+    acc.z += xchg<4>(acc.z);
+    acc.w += xchg<4>(acc.w);
+  }
+  acc.x += xor32(acc.x);
+  acc.y += xor32(acc.y);
+  acc.z += xor32(acc.z);
+  acc.w += xor32(acc.w);
+  // Each row's weight sits in the 4 lanes of a quad: the 64-lane sum is 4x.
+  const float lw = wave_sum(lsum) * 0.25f;
+
+  float a_t = 0.f, m_t = 0.f, l_t = 0.f;  // thread t < D: merged dim t
+  if constexpr (WAVES == 1) {
+    // Lanes 0..G-1 hold dims 4c..4c+3; spread them to threads t < D via LDS.
+    if (lane < G) st4(&s_acc[0][c * 4], acc);
+    __syncthreads();
+    if (tid < D) {
+      a_t = s_acc[0][tid];
+      m_t = mw;
+      l_t = lw;
+    }
+  } else {
+    if (lane < G) st4(&s_acc[wave][c * 4], acc);
+    if (lane == 0) {
+      s_ml[wave][0] = mw;
+      s_ml[wave][1] = lw;
+    }
+    __syncthreads();
+    if (tid < D) {
+      float mm = s_ml[0][0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) mm = fmaxf(mm, s_ml[w][0]);
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float f = fast_exp2(s_ml[w][0] - mm);
+        a_t += f * s_acc[w][tid];
+        l_t += f * s_ml[w][1];
+      }
+      m_t = mm;
+    }
+  }
+
+  if (nsplit == 1) {
+    if (tid < D) outp[tid] = a_t / l_t;
+    return;
+  }
+
+  // Publish this split's partial; the last split of (b, h) to arrive merges.
+  const size_t rec_base = ((size_t)b * p.H + h) * p.nsplit_max * (D + 2);
+  float* rec = p.part + rec_base + (size_t)split * (D + 2);
+  if (tid < D) rec[tid] = a_t;
+  if (tid == 0) {
+    rec[D] = m_t;
+    rec[D + 1] = l_t;
+  }
+  __threadfence();
+  __syncthreads();
+  uint32_t* ctr = p.counters + (size_t)b * p.H + h;
+  if (tid == 0) s_last = (atomicAdd(ctr, 1u) == nsplit - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (tid < D) {
+    const float* base = p.part + rec_base;
+    float mg = -FLT_MAX;
+    for (uint32_t s = 0; s < nsplit; ++s) mg = fmaxf(mg, base[(size_t)s * (D + 2) + D]);
+    float a = 0.f, l = 0.f;
+    for (uint32_t s = 0; s < nsplit; ++s) {
+      const float* r = base + (size_t)s * (D + 2);
+      const float f = fast_exp2(r[D] - mg);
+      a += f * r[tid];
+      l += f * r[D + 1];
+    }
+    outp[tid] = a / l;
+  }
+  if (tid == 0) atomicExch(ctr, 0u);
+}
+
+int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  if (!s || !*s) return dflt;
+  return atoi(s);
+}
+
+}  // namespace
+
+int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
+                  hipStream_t stream) {
+  constexpr uint32_t kRpi = 16;
+  const uint64_t units = (uint64_t)batch * p.H;
+  if (units == 0) return STS_OK;
+  // Small windows (depformer) run one wave per (stream, head); long windows
+  // use 4-wave workgroups and as many splits as it takes to give the chip
+  // about `target` workgroups, with chunks of 64..512 rows.
+  const bool small = max_rows <= 64;
+  const int waves = small ? 1 : 4;
+  const uint32_t unit_rows = waves * kRpi;
+  uint32_t chunk, nsplit;
+  if (small) {
+    chunk = (max_rows + kRpi - 1) / kRpi * kRpi;
+    if (chunk == 0) chunk = kRpi;
+    nsplit = 1;
+  } else {
+    static const int target_mult = env_int("STS_DECODE_WG_PER_CU", 2);
+    static const int chunk_max = env_int("STS_DECODE_CHUNK_MAX", 512);
+    static const int chunk_min = env_int("STS_DECODE_CHUNK_MIN", 64);
+    const uint64_t target = (uint64_t)device_cu_count() * (uint64_t)target_mult;
+    uint64_t want = (target + units - 1) / units;
+    if (want < 1) want = 1;
+    uint64_t c = (max_rows + want - 1) / want;
+    c = (c + unit_rows - 1) / unit_rows * unit_rows;
+    if (c > (uint64_t)chunk_max) c = (uint64_t)chunk_max / unit_rows * unit_rows;
+    if (c < (uint64_t)chunk_min) c = (uint64_t)chunk_min;
+    if (c < unit_rows) c = unit_rows;
+    chunk = (uint32_t)c;
+    nsplit = (max_rows + chunk - 1) / chunk;
+  }
+  p.chunk = chunk;
+  p.nsplit_max = nsplit;
+  if (nsplit > 1) {
+    Workspace* ws = nullptr;
+    const int rc = get_workspace(stream, (size_t)units * nsplit * (head_dim + 2), units, &ws);
+    if (rc != STS_OK) return rc;
+    p.part = ws->part;
+    p.counters = ws->counters;
+  }
+  if (batch > 65535u || p.H > 65535u)
+    return fail(STS_ERR_INVALID, "batch (%u) and heads (%u) must be <= 65535", batch, p.H);
+  const dim3 grid(nsplit, p.H, batch);
+  if (head_dim == 128) {
+    if (waves == 1)
+      hipLaunchKernelGGL((decode_kernel<128, 1>), grid, dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_kernel<128, 4>), grid, dim3(256), 0, stream, p);
+  } else if (head_dim == 64) {
+    if (waves == 1)
+      hipLaunchKernelGGL((decode_kernel<64, 1>), grid, dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_kernel<64, 4>), grid, dim3(256), 0, stream, p);
+  } else {
+    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  }
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+float softmax_scale_log2(float scale) { return scale * kLog2e; }
+
+}  // namespace sts

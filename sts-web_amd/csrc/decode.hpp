@@ -1,0 +1,48 @@
+// decode.hpp -- split-KV decode attention over a ring-buffer KV cache.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sts {
+
+// One launch of the decode kernel.  Row i (0 <= i < len) of stream b, head h
+// lives in slot (start + i) % M of  k + b*kv_bstride + h*kv_hstride  (rows of
+// head_dim floats).  With k_new set, row len-1 is taken from k_new/v_new and
+// written to its slot of k_wr/v_wr (a fused append).
+struct DecodeParams {
+  const float* q = nullptr;      // stream b, head h at q + b*q_bstride + h*D
+  const float* k = nullptr;
+  const float* v = nullptr;
+  float* out = nullptr;          // stream b, head h at out + b*out_bstride + h*D
+  const float* k_new = nullptr;  // same addressing as q, or null
+  const float* v_new = nullptr;
+  float* k_wr = nullptr;
+  float* v_wr = nullptr;
+  const float* rope_cos = nullptr;  // [max_pos][D/2]; with rope, q and k_new are
+  const float* rope_sin = nullptr;  // rotated in registers at position rope_pos
+  const int32_t* lens = nullptr;    // per-stream device arrays, or null for the
+  const int32_t* starts = nullptr;  // uniform len/start below
+  uint32_t len = 0, start = 0;
+  uint32_t rope_pos = 0;
+  uint32_t H = 0, M = 0;
+  uint64_t q_bstride = 0, out_bstride = 0;
+  uint64_t kv_bstride = 0, kv_hstride = 0;
+  float scale_log2 = 0.f;  // softmax scale * log2(e)
+  uint32_t chunk = 0;      // rows per split
+  uint32_t nsplit_max = 1; // grid x
+  float* part = nullptr;   // [B][H][nsplit_max][D+2] partials (nsplit > 1 only)
+  uint32_t* counters = nullptr;  // [B][H] arrival counters, zero between calls
+};
+
+// scale * log2(e), the factor the decode and prefill kernels fold into q.
+float softmax_scale_log2(float scale);
+
+// Chooses chunk / nsplit_max / waves for `units` (stream, head) pairs whose
+// longest window is max_rows, then launches.  Allocates the split workspace
+// from the per-stream pool when more than one split is needed.
+int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
+                  hipStream_t stream);
+
+}  // namespace sts

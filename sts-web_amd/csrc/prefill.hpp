@@ -1,0 +1,25 @@
+// prefill.hpp -- chunked causal prefill attention over a ring-buffer KV cache.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sts {
+
+// Query i (0 <= i < S) is window row len - S + i and attends window rows
+// 0..len-S+i; window row r of head h is slot (start + r) % M of
+// k + h*M*D.  q, out are [S][H][D].
+struct PrefillParams {
+  const float* q = nullptr;
+  const float* k = nullptr;
+  const float* v = nullptr;
+  float* out = nullptr;
+  uint32_t S = 0, H = 0, M = 0;
+  uint32_t start = 0, len = 0;
+  float scale_log2 = 0.f;
+};
+
+int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream);
+
+}  // namespace sts

@@ -1,0 +1,424 @@
+"""Python view of libsts_attn.so, the MI355X attention hot path of sts-web.
+
+This module mirrors the reference's Rust interface for the path
+(crates/sts-wasm/src/model.rs of idle-intelligence/sts-web):
+
+    fused_attention(q, k, v, scale)               model.rs:598-668
+    gpu_cache_write_v(v, cache, offset, max_len)  model.rs:143-188
+    KVCache / LayerCaches                          model.rs:195-411
+    RoPE                                           model.rs:38-122
+
+over the C ABI declared in include/sts_attn.h.  Device memory comes from
+torch tensors (float32, on a ROCm device); every call goes through the HIP
+library, and importing this module without the built library raises.
+Errors from the library raise StsError with the library's message, the
+counterpart of the reference's `.expect(...)` panics.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch  # loaded first so the process has one HIP runtime
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libsts_attn.so")
+
+STS_OK = 0
+STS_ERR_INVALID = -1
+STS_ERR_HIP = -2
+STS_ERR_STATE = -3
+STS_ERR_NOMEM = -4
+PREC_F32 = 0
+PREC_BF16_MFMA = 1
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+
+
+class StsError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"sts_attn error {code}: {msg}")
+        self.code = code
+
+
+class KvState(ctypes.Structure):
+    _fields_ = [("offset", _u64), ("len", _u64), ("write_pos", _u64), ("max_len", _u64),
+                ("heads", _u64), ("head_dim", _u64), ("batch", _u64), ("allocated", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+# name -> (restype, argtypes); the exported set of include/sts_attn.h.
+SIGNATURES = {
+    "sts_last_error": (ctypes.c_char_p, []),
+    "sts_abi_version": (_int, []),
+    "sts_fused_attention": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u64, _vp]),
+    "sts_cache_write": (_int, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "sts_decode_ring": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32, _vp]),
+    "sts_depformer_step": (_int, [_vp, _vp, _vp, _u64, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                  _u32, _f32, _vp]),
+    "sts_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _f32,
+                                     _int, _vp]),
+    "sts_rope_create": (_int, [_u32, _u32, _f32, ctypes.POINTER(_vp)]),
+    "sts_rope_destroy": (_int, [_vp]),
+    "sts_rope_apply": (_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "sts_kv_create": (_int, [_u64, _u64, _u64, ctypes.POINTER(_vp)]),
+    "sts_kv_destroy": (_int, [_vp]),
+    "sts_kv_ensure_allocated": (_int, [_vp, _u64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                       ctypes.POINTER(_u64), _vp]),
+    "sts_kv_get_state": (_int, [_vp, ctypes.POINTER(KvState)]),
+    "sts_kv_window": (_int, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "sts_kv_advance": (_int, [_vp, _u64]),
+    "sts_kv_update": (_int, [_vp, _vp, _vp, _u64, _u64, _vp]),
+    "sts_kv_reset": (_int, [_vp]),
+    "sts_kv_reset_keep_buffers": (_int, [_vp, _vp]),
+    "sts_kv_rollback": (_int, [_vp, _u64]),
+    "sts_kv_attend": (_int, [_vp, _vp, _vp, _f32, _vp]),
+    "sts_kv_decode_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u64, _f32, _vp]),
+    "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
+}
+
+_lib = None
+
+
+def load():
+    """Loads libsts_attn.so (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run `make -C sts-web_amd`)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != STS_OK:
+        msg = load().sts_last_error().decode(errors="replace")
+        raise StsError(rc, msg)
+
+
+def _stream(stream) -> Optional[int]:
+    """hipStream_t of `stream` (a torch stream, an int handle, or None = current)."""
+    if stream is None:
+        if torch.cuda.is_available():
+            return torch.cuda.current_stream().cuda_stream
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None:
+        return None
+    if t.dtype != torch.float32 and t.dtype != torch.int32:
+        raise TypeError(f"expected float32/int32 tensor, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Stateless ops
+# ---------------------------------------------------------------------------
+
+def fused_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                    seq_len: Optional[int] = None, stream=None) -> torch.Tensor:
+    """Decode attention, the fused_attention op (model.rs:598-668).
+
+    q: [1, 1, H, D] (or [H, D]); k, v: [1, H, L, D] cache views -- either
+    contiguous [1, H, S, D] or a [1, H, max_len, D] cache with `seq_len` valid
+    rows (the head stride is taken from the tensor, as the reference reads
+    k.strides[1]).  Returns [1, H, 1, D].
+    """
+    H, D = q.shape[-2], q.shape[-1]
+    if k.dim() == 4:
+        hs = k.stride(1)
+        L = k.shape[2] if seq_len is None else seq_len
+    else:
+        hs = k.stride(0)
+        L = k.shape[1] if seq_len is None else seq_len
+    if k.stride(-1) != 1 or k.stride(-2) != D or v.stride() != k.stride():
+        raise ValueError("k/v rows must be contiguous with identical strides")
+    out = torch.empty((1, H, 1, D), dtype=torch.float32, device=q.device)
+    _check(load().sts_fused_attention(_ptr(q.contiguous()), k.data_ptr(), v.data_ptr(), _ptr(out),
+                                      H, D, L, scale, hs, _stream(stream)))
+    return out
+
+
+def gpu_cache_write_v(v: torch.Tensor, cache: torch.Tensor, offset: int, max_len: int,
+                      stream=None) -> None:
+    """Ring append, gpu_cache_write_v (model.rs:143-188): v [B,S,H,D] -> cache [B,H,M,D]."""
+    B, S, H, D = v.shape
+    if cache.numel() < B * H * max_len * D:
+        raise ValueError("cache smaller than [B, H, max_len, D]")
+    _check(load().sts_cache_write(_ptr(v.contiguous()), _ptr(cache), offset, B, S, H, D, max_len,
+                                  _stream(stream)))
+
+
+def decode_ring(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                lens: torch.Tensor, starts: torch.Tensor, scale: float,
+                out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Ragged multi-stream decode; q [B,H,D], caches [B,H,M,D], lens/starts int32 [B]."""
+    B, H, M, D = k_cache.shape
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.float32, device=q.device)
+    _check(load().sts_decode_ring(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(lens),
+                                  _ptr(starts), B, H, D, M, scale, _stream(stream)))
+    return out
+
+
+def depformer_step(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                   k_cache: torch.Tensor, v_cache: torch.Tensor, step: int, scale: float,
+                   out: Optional[torch.Tensor] = None, qkv_stride: Optional[int] = None,
+                   stream=None) -> torch.Tensor:
+    """Batched depformer step (append at slot `step`, attend slots 0..step).
+
+    q, k_new, v_new: [B, H, D] views whose stream stride is `qkv_stride`
+    elements (default H*D); caches [B, H, max_len, D].
+    """
+    B, H, M, D = k_cache.shape
+    if qkv_stride is None:
+        qkv_stride = q.stride(0)
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.float32, device=k_cache.device)
+    _check(load().sts_depformer_step(q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), qkv_stride,
+                                     _ptr(k_cache), _ptr(v_cache), _ptr(out), B, H, D, M, step,
+                                     scale, _stream(stream)))
+    return out
+
+
+def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      win_start: int, win_len: int, scale: float, precision: int = PREC_F32,
+                      out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Causal chunk attention; q [S,H,D], caches [H,M,D] (or [1,H,M,D])."""
+    S, H, D = q.shape
+    M = k_cache.shape[-2]
+    if out is None:
+        out = torch.empty_like(q)
+    _check(load().sts_prefill_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), S, H, D,
+                                        M, win_start, win_len, scale, precision, _stream(stream)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+class RoPE:
+    """RoPE::new / apply (model.rs:44-121) with tables held by the library."""
+
+    def __init__(self, head_dim: int, max_seq_len: int, theta: float = 10000.0):
+        h = _vp()
+        _check(load().sts_rope_create(head_dim, max_seq_len, theta, ctypes.byref(h)))
+        self._h = h
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+
+    @property
+    def handle(self):
+        return self._h
+
+    def apply_(self, x: torch.Tensor, offset: int, stream=None) -> torch.Tensor:
+        """Rotates x [B,S,H,D] in place at positions offset.. and returns it."""
+        B, S, H, D = x.shape
+        _check(load().sts_rope_apply(self._h, _ptr(x), B, S, H, offset, _stream(stream)))
+        return x
+
+    def apply(self, q: torch.Tensor, k: torch.Tensor, offset: int, stream=None):
+        """Rotated copies of q and k, RoPE::apply (model.rs:111-120)."""
+        return (self.apply_(q.contiguous().clone(), offset, stream),
+                self.apply_(k.contiguous().clone(), offset, stream))
+
+    def close(self):
+        if self._h:
+            load().sts_rope_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# KV cache
+# ---------------------------------------------------------------------------
+
+class KVCache:
+    """Ring-buffer KV cache in HBM, KVCache (model.rs:195-363)."""
+
+    def __init__(self, max_len: int, n_kv_heads: int, head_dim: int):
+        h = _vp()
+        _check(load().sts_kv_create(max_len, n_kv_heads, head_dim, ctypes.byref(h)))
+        self._h = h
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+
+    @property
+    def handle(self):
+        return self._h
+
+    def state(self) -> KvState:
+        s = KvState()
+        _check(load().sts_kv_get_state(self._h, ctypes.byref(s)))
+        return s
+
+    def max_len(self) -> int:
+        return self.state().max_len
+
+    def offset(self) -> int:
+        return self.state().offset
+
+    def seq_len(self) -> int:
+        return self.state().len
+
+    def write_pos(self) -> int:
+        return self.state().write_pos
+
+    def window(self):
+        st, ln = _u64(), _u64()
+        _check(load().sts_kv_window(self._h, ctypes.byref(st), ctypes.byref(ln)))
+        return st.value, ln.value
+
+    def ensure_allocated(self, batch: int, stream=None):
+        """Allocates the buffers if needed; returns (k_ptr, v_ptr, write_pos)."""
+        kp, vp, wp = _vp(), _vp(), _u64()
+        _check(load().sts_kv_ensure_allocated(self._h, batch, ctypes.byref(kp), ctypes.byref(vp),
+                                              ctypes.byref(wp), _stream(stream)))
+        return kp.value, vp.value, wp.value
+
+    def read_buffers(self):
+        """Copies of the K and V buffers as torch tensors [B, H, max_len, D]."""
+        s = self.state()
+        if not s.allocated:
+            return None, None
+        kp, vp, _ = self.ensure_allocated(s.batch)
+        shape = (s.batch, s.heads, s.max_len, s.head_dim)
+        return copy_device(kp, shape), copy_device(vp, shape)
+
+    def advance(self, num_steps: int) -> None:
+        _check(load().sts_kv_advance(self._h, num_steps))
+
+    def update(self, k: torch.Tensor, v: torch.Tensor, stream=None) -> None:
+        """Appends k, v [B, S, H, D] at (offset + s) % max_len and advances S."""
+        B, S, H, D = k.shape
+        _check(load().sts_kv_update(self._h, _ptr(k.contiguous()), _ptr(v.contiguous()), B, S,
+                                    _stream(stream)))
+
+    def reset(self) -> None:
+        _check(load().sts_kv_reset(self._h))
+
+    def reset_keep_buffers(self, stream=None) -> None:
+        _check(load().sts_kv_reset_keep_buffers(self._h, _stream(stream)))
+
+    def rollback(self, n: int) -> None:
+        _check(load().sts_kv_rollback(self._h, n))
+
+    def attend(self, q: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None,
+               stream=None) -> torch.Tensor:
+        """Decode attention over the current window; q [B, H, D] -> [B, H, D]."""
+        if out is None:
+            out = torch.empty_like(q)
+        _check(load().sts_kv_attend(self._h, _ptr(q.contiguous()), _ptr(out), scale,
+                                    _stream(stream)))
+        return out
+
+    def decode_step(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                    scale: float, rope: Optional[RoPE] = None,
+                    out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """Fused RoPE + append + advance(1) + attend; tensors [B, H, D]."""
+        B = q.shape[0]
+        if out is None:
+            out = torch.empty_like(q)
+        _check(load().sts_kv_decode_step(self._h, rope.handle if rope is not None else None,
+                                         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(out), B, scale,
+                                         _stream(stream)))
+        return out
+
+    def prefill(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, scale: float,
+                precision: int = PREC_F32, out: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+        """Appends S rows and runs causal chunk attention; tensors [S, H, D]."""
+        S = q.shape[0]
+        if out is None:
+            out = torch.empty_like(q)
+        _check(load().sts_kv_prefill(self._h, _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(out), S,
+                                     scale, precision, _stream(stream)))
+        return out
+
+    def close(self):
+        if self._h:
+            load().sts_kv_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class LayerCaches:
+    """One KVCache per layer, LayerCaches (model.rs:365-411)."""
+
+    def __init__(self, n_layers: int, max_len: int, n_kv_heads: int, head_dim: int):
+        self.caches = [KVCache(max_len, n_kv_heads, head_dim) for _ in range(n_layers)]
+
+    def get_mut(self, layer: int) -> Optional[KVCache]:
+        return self.caches[layer] if 0 <= layer < len(self.caches) else None
+
+    def seq_len(self) -> int:
+        return self.caches[0].seq_len() if self.caches else 0
+
+    def reset(self) -> None:
+        for c in self.caches:
+            c.reset()
+
+    def reset_keep_buffers(self, stream=None) -> None:
+        for c in self.caches:
+            c.reset_keep_buffers(stream)
+
+    def rollback(self, n: int) -> None:
+        for c in self.caches:
+            c.rollback(n)
+
+
+_hiprt = None
+
+
+def _hip():
+    """The HIP runtime already loaded in this process (torch's), via its soname."""
+    global _hiprt
+    if _hiprt is None:
+        rt = ctypes.CDLL("libamdhip64.so.7")
+        rt.hipMemcpy.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.c_int]
+        rt.hipMemcpy.restype = ctypes.c_int
+        _hiprt = rt
+    return _hiprt
+
+
+def copy_device(ptr: int, shape: Sequence[int]) -> torch.Tensor:
+    """A float32 torch copy of `shape` elements at device address `ptr`."""
+    t = torch.empty(tuple(shape), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    rc = _hip().hipMemcpy(t.data_ptr(), ptr, t.numel() * 4, 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise StsError(STS_ERR_HIP, f"hipMemcpy failed with code {rc}")
+    return t
+
+
+def softmax_scale(head_dim: int) -> float:
+    """head_dim^-0.5 as the reference computes it in f32 (model.rs:705)."""
+    import numpy as np
+    return float(np.float32(head_dim) ** np.float32(-0.5))

@@ -1,0 +1,79 @@
+"""Writes the golden fixtures of tests/golden/ from the CPU oracle.
+
+Run from the repository root after `make -C oracle`:
+    python tests/golden/make_golden.py
+
+Inputs are regenerated at test time from the SplitMix64/Box-Muller spec
+(oracle.normal); each fixture stores the seeds, shapes, the SHA-256 of the
+generated inputs (so a changed generator is caught) and the expected outputs:
+`out_wgsl` (the shader's own f32 order) and `out_f64` (closed form in double).
+RoPE (theta 1e4, interleaved) is applied to Q and K at their logical
+positions, as the configs specify.
+"""
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(HERE))
+import oracle  # noqa: E402
+from cases import decode_inputs, prefill_inputs, scale_for  # noqa: E402
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def decode_case(seed, H, D, M, L, start, rope=True):
+    """One decode: window of L rows at ring slot `start`, query at position L-1."""
+    scale = scale_for(D)
+    q, kc, vc = decode_inputs(seed, H, D, M, L, start, rope)
+    out_w = oracle.attention_ring_wgsl(q, kc, vc, start, L, scale)
+    out_d = oracle.attention_ring_f64(q, kc, vc, start, L, scale)
+    return dict(seed=seed, H=H, D=D, M=M, L=L, start=start, rope=int(rope), scale=scale,
+                input_sha=sha(q, kc, vc), out_wgsl=out_w, out_f64=out_d)
+
+
+def prefill_case(seed, H, D, M, cached, S, start):
+    scale = scale_for(D)
+    L = cached + S
+    q, kc, vc = prefill_inputs(seed, H, D, M, cached, S, start)
+    out_d = oracle.prefill_f64(q, kc, vc, start, L, scale)
+    out_w = oracle.prefill_seq_wgsl(q, kc, vc, start, L, scale)
+    return dict(seed=seed, H=H, D=D, M=M, cached=cached, S=S, start=start, scale=scale,
+                input_sha=sha(q, kc, vc), out_wgsl=out_w, out_f64=out_d)
+
+
+CASES = {
+    # 1 layer, 32 x 128, L = 256, window at slot 0.
+    "decode_config1": lambda: decode_case(101, 32, 128, 256, 256, 0),
+    # Small wrapped windows (both head sizes), L = 1, and a window longer than 256 lanes.
+    "decode_wrap_d64": lambda: decode_case(202, 4, 64, 9, 7, 5),
+    "decode_wrap_d128": lambda: decode_case(303, 3, 128, 40, 33, 29),
+    "decode_len1": lambda: decode_case(404, 2, 128, 16, 1, 11),
+    "decode_long": lambda: decode_case(505, 2, 128, 700, 611, 400),
+    # Depformer-shaped (16 x 64, no RoPE, M = 9).
+    "depformer_step5": lambda: decode_case(606, 16, 64, 9, 6, 0, rope=False),
+    # Chunked prefill, small: 70 new rows after 45 cached, wrapped ring.
+    "prefill_small": lambda: prefill_case(707, 1, 128, 128, 45, 70, 100),
+    "prefill_small_d64": lambda: prefill_case(808, 2, 64, 100, 30, 33, 90),
+}
+
+
+def main():
+    for name, fn in CASES.items():
+        d = fn()
+        path = os.path.join(HERE, f"{name}.npz")
+        np.savez_compressed(path, **{k: np.asarray(v) for k, v in d.items()})
+        print(f"{name}: {os.path.getsize(path)} bytes")
+
+
+if __name__ == "__main__":
+    main()

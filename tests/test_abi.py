@@ -1,0 +1,186 @@
+"""The C ABI on the host (no GPU needed): exports, argument checks, KV counters.
+
+Argument errors are detected before any device work, so they are exercised
+here without a GPU; every one must return a negative status with a message
+and never abort the process.  The KV counter tests restate the reference's
+unit tests (crates/sts-wasm/src/model.rs:1459-1552, depth.rs:1091-1118)
+against the library's KVCache handle; counters move without device buffers.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import oracle
+import sts_attn
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "sts_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sts_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(sts_attn.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = sts_attn.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.sts_abi_version() == 1
+
+
+def _err(rc):
+    assert rc < 0
+    msg = sts_attn.load().sts_last_error().decode()
+    assert msg
+    return msg
+
+
+FAKE = 0x10000  # a 16-byte aligned non-null pointer; never dereferenced
+
+
+def test_fused_attention_argument_errors():
+    lib = sts_attn.load()
+    f = lib.sts_fused_attention
+    assert "null" in _err(f(None, FAKE, FAKE, FAKE, 32, 128, 10, 0.1, 1280, None))
+    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 100, 10, 0.1, 1000, None))
+    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 256, 10, 0.1, 2560, None))
+    assert "seq_len" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 128, 0, 0.1, 1280, None))
+    assert "stride" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 128, 10, 0.1, 128, None))
+    assert "aligned" in _err(f(FAKE + 4, FAKE, FAKE, FAKE, 32, 128, 10, 0.1, 1280, None))
+    assert "scale" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 128, 10, float("nan"), 1280, None))
+
+
+def test_cache_write_argument_errors():
+    f = sts_attn.load().sts_cache_write
+    assert "null" in _err(f(None, FAKE, 0, 1, 1, 32, 128, 3000, None))
+    assert "collide" in _err(f(FAKE, FAKE, 0, 1, 3001, 32, 128, 3000, None))
+    assert "max_len" in _err(f(FAKE, FAKE, 0, 1, 1, 32, 128, 0, None))
+
+
+def test_decode_ring_and_depformer_argument_errors():
+    lib = sts_attn.load()
+    assert "null" in _err(lib.sts_decode_ring(FAKE, FAKE, FAKE, FAKE, None, FAKE, 4, 32, 128,
+                                              3000, 0.1, None))
+    assert "head_dim" in _err(lib.sts_decode_ring(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 96,
+                                                  3000, 0.1, None))
+    assert "step" in _err(lib.sts_depformer_step(FAKE, FAKE, FAKE, 3072, FAKE, FAKE, FAKE, 64,
+                                                 16, 64, 9, 9, 0.125, None))
+    assert "qkv_stride" in _err(lib.sts_depformer_step(FAKE, FAKE, FAKE, 100, FAKE, FAKE, FAKE,
+                                                       64, 16, 64, 9, 0, 0.125, None))
+
+
+def test_prefill_argument_errors():
+    f = sts_attn.load().sts_prefill_attention
+    assert "seq" in _err(f(FAKE, FAKE, FAKE, FAKE, 0, 32, 128, 3000, 0, 768, 0.1, 0, None))
+    assert "seq" in _err(f(FAKE, FAKE, FAKE, FAKE, 800, 32, 128, 3000, 0, 768, 0.1, 0, None))
+    assert "win_len" in _err(f(FAKE, FAKE, FAKE, FAKE, 512, 32, 128, 700, 0, 768, 0.1, 0, None))
+    assert "win_start" in _err(f(FAKE, FAKE, FAKE, FAKE, 512, 32, 128, 3000, 3000, 768, 0.1, 0,
+                                 None))
+    assert "precision" in _err(f(FAKE, FAKE, FAKE, FAKE, 512, 32, 128, 3000, 0, 768, 0.1, 7,
+                                 None))
+
+
+def test_kv_handle_argument_errors():
+    lib = sts_attn.load()
+    h = ctypes.c_void_p()
+    assert "head_dim" in _err(lib.sts_kv_create(3000, 32, 100, ctypes.byref(h)))
+    assert "max_len" in _err(lib.sts_kv_create(0, 32, 128, ctypes.byref(h)))
+    assert "null" in _err(lib.sts_kv_advance(None, 1))
+    c = sts_attn.KVCache(8, 2, 64)
+    # attend before anything was appended: a state error, no device call
+    assert lib.sts_kv_attend(c.handle, FAKE, FAKE, 0.125, None) == sts_attn.STS_ERR_STATE
+    # a chunk longer than the ring is rejected before any allocation
+    assert "seq" in _err(lib.sts_kv_update(c.handle, FAKE, FAKE, 1, 9, None))
+    assert not c.state().allocated
+
+
+def test_rope_argument_errors():
+    lib = sts_attn.load()
+    h = ctypes.c_void_p()
+    assert "head_dim" in _err(lib.sts_rope_create(100, 3000, 1e4, ctypes.byref(h)))
+    assert "theta" in _err(lib.sts_rope_create(128, 3000, -1.0, ctypes.byref(h)))
+    assert "null" in _err(lib.sts_rope_apply(None, FAKE, 1, 1, 32, 0, None))
+
+
+# --- KVCache counters through the C ABI (no device buffers needed) ----------
+
+def test_kv_cache_ring_buffer_counters():
+    """model.rs:1459-1495 with advance() in place of update(): max_len 4."""
+    c = sts_attn.KVCache(4, 2, 64)
+    assert (c.seq_len(), c.offset()) == (0, 0)
+    for i in range(3):
+        c.advance(1)
+        assert c.seq_len() == i + 1
+    assert c.offset() == 3
+    c.advance(1)
+    assert c.seq_len() == 4
+    c.advance(1)
+    assert (c.seq_len(), c.offset()) == (4, 5)
+
+
+def test_kv_cache_reset_counters():
+    """model.rs:1497-1530."""
+    c = sts_attn.KVCache(4, 2, 64)
+    c.advance(1)
+    c.reset()
+    assert (c.seq_len(), c.offset(), c.write_pos()) == (0, 0, 0)
+    c.advance(2)
+    c.reset_keep_buffers()
+    assert (c.seq_len(), c.offset()) == (0, 0)
+    assert not c.state().allocated
+
+
+def test_layer_caches_counters():
+    """model.rs:1532-1552: LayerCaches::seq_len follows layer 0."""
+    lc = sts_attn.LayerCaches(3, 10, 2, 64)
+    assert lc.seq_len() == 0
+    lc.get_mut(0).advance(1)
+    assert lc.seq_len() == 1
+    assert lc.get_mut(3) is None
+    lc.reset()
+    assert lc.seq_len() == 0
+
+
+def test_depformer_cache_counters():
+    """depth.rs:1091-1118: cache (20, 2, 32-dim in the reference; 64 here)."""
+    c = sts_attn.KVCache(20, 2, 64)
+    for i in range(3):
+        c.advance(1)
+        assert c.seq_len() == i + 1
+    c.reset_keep_buffers()
+    assert c.seq_len() == 0
+
+
+@pytest.mark.parametrize("M", [1, 4, 9, 3000])
+def test_counters_match_oracle_over_random_walk(M):
+    """Any sequence of advance / rollback / reset agrees with the oracle's
+    restatement of model.rs:293-362, and the window start stays in range."""
+    import random
+    rnd = random.Random(M)
+    c = sts_attn.KVCache(M, 1, 64)
+    o = oracle.KvCounters(M)
+    for _ in range(400):
+        op = rnd.random()
+        if op < 0.6:
+            n = rnd.randint(0, 2 * M + 3)
+            c.advance(n)
+            o.advance(n)
+        elif op < 0.95:
+            n = rnd.randint(0, M + 2)
+            c.rollback(n)
+            o.rollback(n)
+        else:
+            c.reset()
+            o.reset()
+        s = c.state()
+        assert (s.offset, s.len, s.write_pos) == (o.offset, o.len, o.write_pos)
+        start, ln = c.window()
+        assert ln == o.len and start == o.window_start() and 0 <= start < M

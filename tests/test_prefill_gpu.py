@@ -1,0 +1,103 @@
+"""Chunked causal prefill on the GPU against the oracle.
+
+f32 variant within 1e-4 of the oracle; bf16-MFMA variant within 2e-2 (the
+north star's bars).  The reference executes a prefill as S sequential
+decodes (stream.rs:482-492), so the chunked result is also checked against
+the GPU's own decode over each query's prefix.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sts_attn
+from cases import prefill_inputs, scale_for
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def run(q, kc, vc, start, L, scale, prec):
+    return host(sts_attn.prefill_attention(dev(q), dev(kc), dev(vc), start, L, scale, prec))
+
+
+@pytest.mark.parametrize("name", ["prefill_small", "prefill_small_d64"])
+def test_prefill_fixtures(gpu, name):
+    f = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    args = [int(f[k]) for k in ("seed", "H", "D", "M", "cached", "S", "start")]
+    q, kc, vc = prefill_inputs(*args)
+    L = args[4] + args[5]
+    got = run(q, kc, vc, args[6], L, float(f["scale"]), sts_attn.PREC_F32)
+    assert np.abs(got - f["out_f64"]).max() < TOL_F32
+    assert np.abs(got - f["out_wgsl"]).max() < TOL_F32
+    got = run(q, kc, vc, args[6], L, float(f["scale"]), sts_attn.PREC_BF16_MFMA)
+    assert np.abs(got - f["out_f64"]).max() < TOL_BF16
+
+
+@pytest.mark.parametrize("H,D,M,cached,S,start", [
+    (32, 128, 3000, 256, 512, 2900),  # BASELINE config 3 shape, wrapped window
+    (4, 128, 300, 0, 300, 0),         # empty cache, full ring
+    (3, 64, 200, 17, 1, 190),         # single query == decode
+    (2, 128, 1000, 100, 65, 950),     # ragged last q-tile
+    (2, 64, 129, 64, 65, 100),        # chunk evicts nothing, wraps
+])
+@pytest.mark.parametrize("prec", [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA])
+def test_prefill_against_f64(gpu, H, D, M, cached, S, start, prec):
+    q, kc, vc = prefill_inputs(4000 + S, H, D, M, cached, S, start)
+    L = cached + S
+    got = run(q, kc, vc, start, L, scale_for(D), prec)
+    ref = oracle.prefill_f64(q, kc, vc, start, L, scale_for(D))
+    err = np.abs(got - ref).max()
+    print(f"prefill H{H} D{D} S{S} cached{cached} prec{prec}: max-abs {err:.2e}", flush=True)
+    assert err < (TOL_F32 if prec == sts_attn.PREC_F32 else TOL_BF16)
+
+
+def test_chunked_equals_sequential_decode_on_gpu(gpu):
+    """Row i of the chunk == the GPU decode over the first cached+i+1 rows."""
+    H, D, M, cached, S, start = 32, 128, 3000, 256, 512, 2900
+    q, kc, vc = prefill_inputs(77, H, D, M, cached, S, start)
+    L = cached + S
+    chunk = run(q, kc, vc, start, L, scale_for(D), sts_attn.PREC_F32)
+    kd, vd = dev(kc)[None], dev(vc)[None]
+    for i in (0, 1, 63, 64, 255, 511):
+        lens = torch.tensor([cached + i + 1], dtype=torch.int32, device="cuda")
+        st = torch.tensor([start], dtype=torch.int32, device="cuda")
+        dec = host(sts_attn.decode_ring(dev(q[i])[None], kd, vd, lens, st, scale_for(D)))[0]
+        assert np.abs(chunk[i] - dec).max() < TOL_F32, i
+
+
+def test_kv_prefill_appends_and_attends(gpu):
+    """KVCache.prefill: the chunk lands at (offset + s) % max_len bit for bit, and
+    the result equals prefill_attention over the grown window."""
+    H, D, M = 8, 128, 300
+    c = sts_attn.KVCache(M, H, D)
+    o = oracle.KvCounters(M)
+    kref = np.zeros((1, H, M, D), np.float32)
+    vref = np.zeros((1, H, M, D), np.float32)
+    for it, S in enumerate((200, 150, 64, 1)):
+        q = oracle.normal(10 + it, (S, H, D))
+        k = oracle.normal(20 + it, (S, H, D))
+        v = oracle.normal(30 + it, (S, H, D))
+        got = host(c.prefill(dev(q), dev(k), dev(v), scale_for(D)))
+        oracle.cache_write(k[None], kref, o.offset % M, M)
+        oracle.cache_write(v[None], vref, o.offset % M, M)
+        o.advance(S)
+        kb, vb = c.read_buffers()
+        np.testing.assert_array_equal(host(kb), kref)
+        np.testing.assert_array_equal(host(vb), vref)
+        ref = oracle.prefill_f64(q, kref[0], vref[0], o.window_start(), o.len, scale_for(D))
+        assert np.abs(got - ref).max() < TOL_F32, it
