@@ -1,0 +1,337 @@
+"""Benchmark of the sts-web attention hot path on one MI355X.
+
+Headline: one temporal frame = 24 sequential layer
+decode steps, each a fused append + attention (sts_kv_decode_step) over a
+32-head x 128 f32 ring cache holding 3000 rows, with the write head at a
+seeded offset so reads wrap.  Every layer has its own 98 MB cache (2.36 GB,
+beyond the 256 MB MALL).  Inputs are resident in HBM before timing.
+
+Also reported (extra fields): decode without the append (sts_kv_attend),
+chunked prefill (config 3, f32 and bf16-MFMA), depformer frame (config 4) and
+ragged multi-stream decode (config 5); and the CPU baseline -- the oracle's
+restatement of the reference shader, timed on this host's cores on a bounded
+sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode]
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sts-web_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3       # fp32 MFMA
+
+LAYERS, H, D, M = 24, 32, 128, 3000
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="", help="comma list of sections to run")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def __enter__(self):
+        self.torch.cuda.synchronize()
+        self.a = self.torch.cuda.Event(enable_timing=True)
+        self.b = self.torch.cuda.Event(enable_timing=True)
+        self.a.record(self.stream)
+        return self
+
+    def __exit__(self, *exc):
+        self.b.record(self.stream)
+        self.torch.cuda.synchronize()
+        self.ms = self.a.elapsed_time(self.b)
+
+
+def bench_decode(torch, sts, stream, steps, warmup):
+    """Config 2: returns dict with per-frame and per-launch timings."""
+    scale = sts.softmax_scale(D)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    caches = []
+    rows = torch.empty((1, M, H, D), device="cuda")
+    for layer in range(LAYERS):
+        c = sts.KVCache(M, H, D)
+        # Seeded write head: advance the empty ring, then append 3000 rows
+        # from there, so the window starts mid-buffer and reads wrap.
+        c.advance((layer * 997 + 123) % M)
+        rows.normal_(generator=g)
+        krows = rows.clone()
+        rows.normal_(generator=g)
+        c.update(krows, rows, stream)
+        assert c.seq_len() == M and c.window()[0] != 0
+        caches.append(c)
+    q = torch.randn((LAYERS, 1, H, D), generator=g, device="cuda")
+    kn = torch.randn((LAYERS, 1, H, D), generator=g, device="cuda")
+    vn = torch.randn((LAYERS, 1, H, D), generator=g, device="cuda")
+    out = torch.empty((LAYERS, 1, H, D), device="cuda")
+
+    def frame():
+        for layer in range(LAYERS):
+            caches[layer].decode_step(q[layer], kn[layer], vn[layer], scale, out=out[layer],
+                                      stream=stream)
+
+    def frame_attend():
+        for layer in range(LAYERS):
+            caches[layer].attend(q[layer], scale, out=out[layer], stream=stream)
+
+    for _ in range(warmup):
+        frame()
+    with Timer(torch, stream) as t:
+        for _ in range(steps):
+            frame()
+    for _ in range(2):
+        frame_attend()
+    with Timer(torch, stream) as ta:
+        for _ in range(steps):
+            frame_attend()
+    bytes_layer = 2 * M * H * D * 4 + 2 * H * D * 4   # K/V reads + Q read + O write
+    us_frame = t.ms * 1e3 / steps
+    us_launch = us_frame / LAYERS
+    us_attend = ta.ms * 1e3 / steps / LAYERS
+    return {
+        "us_per_frame": us_frame,
+        "us_per_launch": us_launch,
+        "bytes_per_launch": bytes_layer,
+        "gbs": bytes_layer / (us_launch * 1e-6) / 1e9,
+        "attend_only_us_per_launch": us_attend,
+        "attend_only_gbs": bytes_layer / (us_attend * 1e-6) / 1e9,
+        "caches": caches,
+        "q": q,
+    }
+
+
+def bench_prefill(torch, sts, stream, steps, warmup):
+    """Config 3: 512 new rows after 256 cached, 24 layers, f32 and bf16-MFMA."""
+    cached, S = 256, 512
+    L = cached + S
+    scale = sts.softmax_scale(D)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    kc = torch.randn((LAYERS, H, M, D), generator=g, device="cuda")
+    vc = torch.randn((LAYERS, H, M, D), generator=g, device="cuda")
+    q = torch.randn((LAYERS, S, H, D), generator=g, device="cuda")
+    out = torch.empty_like(q)
+    starts = [(2900 + 37 * i) % M for i in range(LAYERS)]
+    pairs = S * cached + S * (S + 1) // 2
+    flops_layer = 4 * H * D * pairs
+    res = {"flops_per_layer": flops_layer}
+    for name, prec in (("bf16", sts.PREC_BF16_MFMA), ("f32", sts.PREC_F32)):
+        def run():
+            for layer in range(LAYERS):
+                sts.prefill_attention(q[layer], kc[layer], vc[layer], starts[layer], L, scale,
+                                      prec, out=out[layer], stream=stream)
+        for _ in range(warmup):
+            run()
+        with Timer(torch, stream) as t:
+            for _ in range(steps):
+                run()
+        us_layer = t.ms * 1e3 / steps / LAYERS
+        res[name] = {"us_per_layer": us_layer,
+                     "tflops": flops_layer / (us_layer * 1e-6) / 1e12}
+    return res
+
+
+def bench_depformer(torch, sts, stream, steps, warmup):
+    """Config 4: 6 layers x 8 steps, 64 streams, 16 x 64, M = 9."""
+    B, Hd, Dd, Md, layers, nsteps = 64, 16, 64, 9, 6, 8
+    scale = sts.softmax_scale(Dd)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    qkv = torch.randn((nsteps, layers, B, 3, Hd, Dd), generator=g, device="cuda")
+    kc = torch.zeros((layers, B, Hd, Md, Dd), device="cuda")
+    vc = torch.zeros((layers, B, Hd, Md, Dd), device="cuda")
+    out = torch.empty((B, Hd, Dd), device="cuda")
+
+    def frame():
+        for step in range(nsteps):
+            for layer in range(layers):
+                x = qkv[step, layer]
+                sts.depformer_step(x[:, 0], x[:, 1], x[:, 2], kc[layer], vc[layer], step, scale,
+                                   out=out, qkv_stride=3 * Hd * Dd, stream=stream)
+
+    for _ in range(warmup):
+        frame()
+    with Timer(torch, stream) as t:
+        for _ in range(steps):
+            frame()
+    us_frame = t.ms * 1e3 / steps
+    kv_bytes = sum(2 * B * Hd * (s + 1) * Dd * 4 for s in range(nsteps)) * layers
+    return {"us_per_frame": us_frame, "launches_per_frame": nsteps * layers,
+            "us_per_launch": us_frame / (nsteps * layers),
+            "kv_read_gbs": kv_bytes / (us_frame * 1e-6) / 1e9}
+
+
+def bench_ragged(torch, sts, stream, steps, warmup):
+    """Config 5: 64 streams x 32 x 128, L ~ U[128, 3000], wrapped starts; 24
+    layers cycling over 2 cache slabs (12.6 GB, beyond the MALL)."""
+    B = 64
+    scale = sts.softmax_scale(D)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    slabs = []
+    for _ in range(2):
+        kc = torch.randn((B, H, M, D), generator=g, device="cuda")
+        vc = torch.randn((B, H, M, D), generator=g, device="cuda")
+        slabs.append((kc, vc))
+    lens = torch.randint(128, 3001, (LAYERS, B), generator=g, device="cuda", dtype=torch.int32)
+    starts = torch.randint(0, M, (LAYERS, B), generator=g, device="cuda", dtype=torch.int32)
+    q = torch.randn((B, H, D), generator=g, device="cuda")
+    out = torch.empty((B, H, D), device="cuda")
+
+    def frame():
+        for layer in range(LAYERS):
+            kc, vc = slabs[layer % 2]
+            sts.decode_ring(q, kc, vc, lens[layer], starts[layer], scale, out=out, stream=stream)
+
+    for _ in range(warmup):
+        frame()
+    with Timer(torch, stream) as t:
+        for _ in range(steps):
+            frame()
+    total_rows = int(lens.sum().item())
+    bytes_frame = total_rows * H * D * 4 * 2 + LAYERS * 2 * B * H * D * 4
+    us_frame = t.ms * 1e3 / steps
+    return {"us_per_frame": us_frame, "us_per_layer": us_frame / LAYERS,
+            "gbs": bytes_frame / (us_frame * 1e-6) / 1e9,
+            "mean_len": total_rows / (LAYERS * B)}
+
+
+def cpu_baseline(torch, dec):
+    """The oracle's restatement of shader_attention.wgsl, on this host's cores,
+    over 2 of the 24 layers of the decode workload, scaled to us/frame."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    cores = min(os.cpu_count() or 1, 16)
+    oracle.set_num_threads(cores)
+    n_layers = 2
+    scale = float(np.float32(D) ** np.float32(-0.5))
+    times = []
+    for layer in range(n_layers):
+        c = dec["caches"][layer]
+        kb, vb = c.read_buffers()
+        start, ln = c.window()
+        kc = kb[0].cpu().numpy()
+        vc = vb[0].cpu().numpy()
+        qh = dec["q"][layer, 0].cpu().numpy()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            oracle.attention_ring_wgsl(qh, kc, vc, start, ln, scale)
+        times.append((time.perf_counter() - t0) / 3)
+    us_layer = float(np.median(times)) * 1e6
+    return {"value": us_layer * LAYERS, "unit": "us/frame", "cores": cores, "kind": "port",
+            "sample": f"{n_layers} of {LAYERS} layers (32 heads x 3000 rows each, 3 runs), "
+                      f"oracle shader-order f32 attention, OpenMP over heads, scaled x{LAYERS}",
+            "us_per_layer": us_layer}
+
+
+def load_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
+              f"(the path shards by head or stream; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import sts_attn as sts
+    sts.load()
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda s: not only or s in only)
+    stream = torch.cuda.Stream()
+    extra = {}
+    with torch.cuda.stream(stream):
+        log("bench: decode (config 2)")
+        dec = bench_decode(torch, sts, stream, args.steps, args.warmup)
+        if want("prefill"):
+            log("bench: prefill (config 3)")
+            extra["prefill"] = bench_prefill(torch, sts, stream, args.steps, args.warmup)
+        if want("depformer"):
+            log("bench: depformer (config 4)")
+            extra["depformer"] = bench_depformer(torch, sts, stream, args.steps, args.warmup)
+        if want("ragged"):
+            log("bench: ragged (config 5)")
+            extra["ragged"] = bench_ragged(torch, sts, stream, max(2, args.steps // 4),
+                                           min(args.warmup, 2))
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(torch, dec)
+    achieved = dec["gbs"]
+    line = {
+        "metric": "decode attn us/frame (24L, KV 3000) + achieved HBM GB/s; prefill TFLOP/s",
+        "value": round(dec["us_per_frame"], 2),
+        "unit": "us/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["us_per_frame"] / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (torch.randn, seeded), inputs resident in HBM",
+        "config": {"workload": "temporal decode frame: 24 layers x fused append+attention, "
+                               "32 heads x 128, f32 ring KV cache of 3000 rows (wrapped), batch 1",
+                   "layers": LAYERS, "heads": H, "head_dim": D, "kv_len": M},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(),
+                     "kernel": "decode_kernel<128,4>",
+                     "bytes_per_launch": dec["bytes_per_launch"],
+                     "us_per_launch": round(dec["us_per_launch"], 3)},
+        "cpu_baseline": cpu,
+        "decode_attend_only": {"us_per_launch": round(dec["attend_only_us_per_launch"], 3),
+                               "gbs": round(dec["attend_only_gbs"], 1)},
+    }
+    if "prefill" in extra:
+        p = extra["prefill"]
+        line["prefill"] = {
+            "flops_per_layer": p["flops_per_layer"],
+            "bf16_us_per_layer": round(p["bf16"]["us_per_layer"], 3),
+            "bf16_tflops": round(p["bf16"]["tflops"], 1),
+            "bf16_frac_of_mfma_peak": round(p["bf16"]["tflops"] / BF16_PEAK_TFLOPS, 4),
+            "f32_us_per_layer": round(p["f32"]["us_per_layer"], 3),
+            "f32_tflops": round(p["f32"]["tflops"], 1),
+            "f32_frac_of_fp32_peak": round(p["f32"]["tflops"] / FP32_PEAK_TFLOPS, 4)}
+    if "depformer" in extra:
+        line["depformer"] = {k: round(v, 3) for k, v in extra["depformer"].items()}
+    if "ragged" in extra:
+        r = extra["ragged"]
+        line["ragged"] = {k: round(v, 2) for k, v in r.items()}
+        line["ragged"]["frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    if cpu is not None:
+        line["gpu_vs_cpu"] = round(cpu["value"] / dec["us_per_frame"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

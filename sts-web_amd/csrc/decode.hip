@@ -28,11 +28,24 @@ namespace sts {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxSplits = 64;  // splits per (stream, head), bounded by the merge's LDS
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+// Split partials travel between workgroups (possibly on different XCDs, each
+// with its own L2) through accesses that carry device (agent) coherence scope
+// themselves -- global_store/global_load with sc1 -- so publishing them needs
+// only a wait for their acknowledgement, not an L2 write-back or invalidate
+// of everything the workgroup has touched.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Interleaved RoPE of two adjacent pairs (model.rs:99-100), each product and
 // sum rounded separately as the reference evaluates them.
@@ -110,6 +123,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   __shared__ __align__(16) float s_p[WAVES][RPI];
   __shared__ __align__(16) float s_acc[WAVES][D];
   __shared__ float s_ml[WAVES][2];
+  __shared__ __align__(16) float s_red[WAVES * 64 * 4];  // split-merge partial sums
+  __shared__ float s_sm[kMaxSplits], s_sl[kMaxSplits];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -255,69 +270,94 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // Each row's weight sits in the 4 lanes of a quad: the 64-lane sum is 4x.
   const float lw = wave_sum(lsum) * 0.25f;
 
-  float a_t = 0.f, m_t = 0.f, l_t = 0.f;  // thread t < D: merged dim t
-  if constexpr (WAVES == 1) {
-    // Lanes 0..G-1 hold dims 4c..4c+3; spread them to threads t < D via LDS.
-    if (lane < G) st4(&s_acc[0][c * 4], acc);
-    __syncthreads();
-    if (tid < D) {
-      a_t = s_acc[0][tid];
-      m_t = mw;
-      l_t = lw;
-    }
-  } else {
-    if (lane < G) st4(&s_acc[wave][c * 4], acc);
-    if (lane == 0) {
-      s_ml[wave][0] = mw;
-      s_ml[wave][1] = lw;
-    }
-    __syncthreads();
-    if (tid < D) {
-      float mm = s_ml[0][0];
+  // Merge the waves: every thread computes the common max and sum, then the
+  // dims t = tid, tid + NT, ... (NT may be smaller than D).
+  constexpr int NT = WAVES * 64;
+  if (lane < G) st4(&s_acc[wave][c * 4], acc);
+  if (lane == 0) {
+    s_ml[wave][0] = mw;
+    s_ml[wave][1] = lw;
+  }
+  __syncthreads();
+  float m_t = s_ml[0][0];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) mm = fmaxf(mm, s_ml[w][0]);
+  for (int w = 1; w < WAVES; ++w) m_t = fmaxf(m_t, s_ml[w][0]);
+  float fw[WAVES];
+  float l_t = 0.f;
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const float f = fast_exp2(s_ml[w][0] - mm);
-        a_t += f * s_acc[w][tid];
-        l_t += f * s_ml[w][1];
-      }
-      m_t = mm;
-    }
+  for (int w = 0; w < WAVES; ++w) {
+    fw[w] = fast_exp2(s_ml[w][0] - m_t);
+    l_t += fw[w] * s_ml[w][1];
   }
 
   if (nsplit == 1) {
-    if (tid < D) outp[tid] = a_t / l_t;
+    for (int t = tid; t < D; t += NT) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) a += fw[w] * s_acc[w][t];
+      outp[t] = a / l_t;
+    }
     return;
   }
 
   // Publish this split's partial; the last split of (b, h) to arrive merges.
-  const size_t rec_base = ((size_t)b * p.H + h) * p.nsplit_max * (D + 2);
-  float* rec = p.part + rec_base + (size_t)split * (D + 2);
-  if (tid < D) rec[tid] = a_t;
-  if (tid == 0) {
-    rec[D] = m_t;
-    rec[D + 1] = l_t;
+  // Records are acc[D], m, l and 2 pad floats.
+  constexpr int REC = D + 4;
+  const size_t rec_base = ((size_t)b * p.H + h) * p.nsplit_max * REC;
+  float* rec = p.part + rec_base + (size_t)split * REC;
+  for (int t = tid; t < D; t += NT) {
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) a += fw[w] * s_acc[w][t];
+    st_agent(rec + t, a);
   }
-  __threadfence();
+  if (tid == 0) {
+    st_agent(rec + D, m_t);
+    st_agent(rec + D + 1, l_t);
+  }
+  // Each wave waits until its device-coherent stores are acknowledged; after
+  // the barrier the whole partial is visible device-wide, then one thread
+  // counts the arrival (a device-scope atomic).  The workgroup fences inside
+  // __syncthreads keep the compiler from moving the atomics across it.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   uint32_t* ctr = p.counters + (size_t)b * p.H + h;
   if (tid == 0) s_last = (atomicAdd(ctr, 1u) == nsplit - 1);
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  if (tid < D) {
-    const float* base = p.part + rec_base;
-    float mg = -FLT_MAX;
-    for (uint32_t s = 0; s < nsplit; ++s) mg = fmaxf(mg, base[(size_t)s * (D + 2) + D]);
-    float a = 0.f, l = 0.f;
-    for (uint32_t s = 0; s < nsplit; ++s) {
-      const float* r = base + (size_t)s * (D + 2);
-      const float f = fast_exp2(r[D] - mg);
-      a += f * r[tid];
-      l += f * r[D + 1];
-    }
-    outp[tid] = a / l;
+
+  // Merge all splits: one round trip for the (m, l) pairs, one for the
+  // accumulators, spread over the workgroup as float4 columns x split groups.
+  const float* base = p.part + rec_base;
+  for (uint32_t s = tid; s < nsplit; s += NT) {
+    s_sm[s] = ld_agent(base + (size_t)s * REC + D);
+    s_sl[s] = ld_agent(base + (size_t)s * REC + D + 1);
+  }
+  __syncthreads();
+  float mg = -FLT_MAX;
+  for (uint32_t s = 0; s < nsplit; ++s) mg = fmaxf(mg, s_sm[s]);
+  float l = 0.f;
+  for (uint32_t s = 0; s < nsplit; ++s) l += fast_exp2(s_sm[s] - mg) * s_sl[s];
+  constexpr int C4 = D / 4;
+  constexpr int NSG = NT / C4;
+  const int c4 = tid % C4, sg = tid / C4;
+  float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (uint32_t s = sg; s < nsplit; s += NSG) {
+    const float f = fast_exp2(s_sm[s] - mg);
+    const float* r = base + (size_t)s * REC + c4 * 4;
+    a4.x += f * ld_agent(r);
+    a4.y += f * ld_agent(r + 1);
+    a4.z += f * ld_agent(r + 2);
+    a4.w += f * ld_agent(r + 3);
+  }
+  st4(&s_red[sg * D + c4 * 4], a4);
+  __syncthreads();
+  for (int t = tid; t < D; t += NT) {
+    float a = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < NSG; ++g2) a += s_red[g2 * D + t];
+    outp[t] = a / l;
   }
   if (tid == 0) atomicExch(ctr, 0u);
 }
@@ -360,12 +400,17 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
     if (c < unit_rows) c = unit_rows;
     chunk = (uint32_t)c;
     nsplit = (max_rows + chunk - 1) / chunk;
+    if (nsplit > (uint32_t)kMaxSplits) {
+      chunk = (max_rows + kMaxSplits - 1) / kMaxSplits;
+      chunk = (chunk + unit_rows - 1) / unit_rows * unit_rows;
+      nsplit = (max_rows + chunk - 1) / chunk;
+    }
   }
   p.chunk = chunk;
   p.nsplit_max = nsplit;
   if (nsplit > 1) {
     Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)units * nsplit * (head_dim + 2), units, &ws);
+    const int rc = get_workspace(stream, (size_t)units * nsplit * (head_dim + 4), units, &ws);
     if (rc != STS_OK) return rc;
     p.part = ws->part;
     p.counters = ws->counters;

@@ -32,7 +32,7 @@ struct DecodeParams {
   float scale_log2 = 0.f;  // softmax scale * log2(e)
   uint32_t chunk = 0;      // rows per split
   uint32_t nsplit_max = 1; // grid x
-  float* part = nullptr;   // [B][H][nsplit_max][D+2] partials (nsplit > 1 only)
+  float* part = nullptr;   // [B][H][nsplit_max][D+4] partials (nsplit > 1 only)
   uint32_t* counters = nullptr;  // [B][H] arrival counters, zero between calls
 };
 

@@ -95,6 +95,8 @@ def test_update_sequence_matches_oracle_with_rollbacks(gpu):
         kb, vb = c.read_buffers()
         np.testing.assert_array_equal(host(kb), kref)
         np.testing.assert_array_equal(host(vb), vref)
+        if o.len == 0:
+            continue
         q = oracle.normal(7000 + it, (1, H, D))
         got = host(c.attend(dev(q), scale_for(D)))[0]
         ref = oracle.attention_ring_f64(q[0], kref[0], vref[0], o.window_start(), o.len,
