@@ -2,11 +2,11 @@
 //
 // Replaces shader_attention.wgsl (crates/sts-wasm/src/wgsl/shader_attention.wgsl:43-156),
 // which runs one 256-lane workgroup per head, each lane streaming whole
-// 512-byte rows.  Here the window of every (stream, head) is cut into splits
-// of `chunk` rows; each workgroup streams one split with 128-bit loads that
-// are contiguous across lanes, keeps an online softmax per row group, merges
-// its waves through LDS, and the last workgroup of a (stream, head) to finish
-// merges the splits (log-sum-exp) and writes the output.
+// 512-byte rows.  Here the window of every (stream, head) is dealt to splits
+// in 16-row units, round-robin; each workgroup streams one split with 128-bit
+// loads that are contiguous across lanes, keeps an online softmax per row
+// group, merges its waves through LDS, and the last workgroup of a
+// (stream, head) to finish merges the splits (log-sum-exp) and writes out.
 //
 // Layout per wave (D = head_dim, G = D/4 lanes per row, NG = 64/G row groups):
 //   lane = g*G + c holds dims [4c, 4c+4) of the rows of group g; one loop
@@ -112,7 +112,7 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-template <int D, int WAVES>
+template <int D, int WAVES, bool PIPE>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p) {
   constexpr int G = D / 4;
   constexpr int NG = 64 / G;
@@ -151,10 +151,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       for (int t = tid; t < D; t += WAVES * 64) outp[t] = 0.f;
     return;
   }
-  const uint32_t i0 = split * p.chunk;
-  if (i0 >= len) return;
-  const uint32_t i1 = min(len, i0 + p.chunk);
-  const uint32_t nsplit = (len + p.chunk - 1) / p.chunk;
+  // This (stream, head) gets ceil(len / chunk) splits (at most nsplit_max);
+  // split s takes the 16-row units s, s + nsplit, ... so that every
+  // workgroup streams from the whole window and XCDs share the load evenly.
+  uint32_t nsplit = (len + p.chunk - 1) / p.chunk;
+  nsplit = nsplit < p.nsplit_max ? nsplit : p.nsplit_max;
+  if (split >= nsplit) return;
+  const uint32_t nunits = (len + RPI - 1) / RPI;
 
   const size_t qoff = b * p.q_bstride + (size_t)h * D + c * 4;
   float4 q4 = ld4(p.q + qoff);
@@ -182,14 +185,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   const int jj = (c >> 2) & (RPG - 1);
 
-  for (uint32_t r0 = i0 + wave * RPI; r0 < i1; r0 += WAVES * RPI) {
-    float4 kk[RPG], vv[RPG];
+  // Loads rows r0 + j*NG + g (j < RPG) of this lane's group into kk/vv; the
+  // fused-append row is taken from k_new/v_new and written to its slot.
+  auto load_rows = [&](uint32_t r0, float4* kk, float4* vv) {
 #pragma unroll
     for (int j = 0; j < RPG; ++j) {
       const uint32_t r = r0 + j * NG + g;
       uint32_t slot = start + r;
       slot = slot >= p.M ? slot - p.M : slot;
-      if (r < i1) {
+      if (r < len) {
         if (append && r == new_row) {
           float4 kn = ld4(p.k_new + qoff);
           const float4 vn = ld4(p.v_new + qoff);
@@ -207,13 +211,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
         vv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
+  };
+  // Online-softmax update with the 16 rows starting at r0.
+  auto consume_rows = [&](uint32_t r0, const float4* kk, const float4* vv) {
     float s[RPG];
 #pragma unroll
     for (int j = 0; j < RPG; ++j)
       s[j] = q4.x * kk[j].x + q4.y * kk[j].y + q4.z * kk[j].z + q4.w * kk[j].w;
     float sc = reduce_rows<G>(s, c);
     const uint32_t my_row = r0 + jj * NG + g;
-    sc = my_row < i1 ? sc : -INFINITY;
+    sc = my_row < len ? sc : -INFINITY;
     const float mn = fmaxf(m, group_max<G>(sc));
     const float alpha = fast_exp2(m - mn);
     const float pj = fast_exp2(sc - mn);
@@ -242,6 +249,31 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       acc.y += pp[j] * vv[j].y;
       acc.z += pp[j] * vv[j].z;
       acc.w += pp[j] * vv[j].w;
+    }
+  };
+
+  const uint32_t ustep = nsplit * WAVES;
+  uint32_t u = split + nsplit * wave;
+  if constexpr (PIPE) {
+    // Two register buffers: the next 16 rows are in flight while the current
+    // 16 are consumed, so each wave always has a full batch of loads queued.
+    float4 ka[RPG], va[RPG], kb[RPG], vb[RPG];
+    if (u < nunits) load_rows(u * RPI, ka, va);
+    while (u < nunits) {
+      const uint32_t u1 = u + ustep;
+      if (u1 < nunits) load_rows(u1 * RPI, kb, vb);
+      consume_rows(u * RPI, ka, va);
+      if (u1 >= nunits) break;
+      const uint32_t u2 = u1 + ustep;
+      if (u2 < nunits) load_rows(u2 * RPI, ka, va);
+      consume_rows(u1 * RPI, kb, vb);
+      u = u2;
+    }
+  } else {
+    for (; u < nunits; u += ustep) {
+      float4 kk[RPG], vv[RPG];
+      load_rows(u * RPI, kk, vv);
+      consume_rows(u * RPI, kk, vv);
     }
   }
 
@@ -300,6 +332,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     return;
   }
 
+  // One-wave launches (windows of at most 64 rows) always run a single split.
+  if constexpr (WAVES == 1) return;
+
   // Publish this split's partial; the last split of (b, h) to arrive merges.
   // Records are acc[D], m, l and 2 pad floats.
   constexpr int REC = D + 4;
@@ -326,9 +361,27 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   __syncthreads();
   if (!s_last) return;
 
-  // Merge all splits: one round trip for the (m, l) pairs, one for the
-  // accumulators, spread over the workgroup as float4 columns x split groups.
+  // Merge all splits in one round trip: the (m, l) pairs go to LDS while each
+  // thread holds the raw accumulators of its float4 column for the splits
+  // sg, sg + NSG, ...; weights are applied once the global max is known.
   const float* base = p.part + rec_base;
+  constexpr int C4 = D / 4;
+  constexpr int NSG = NT / C4;
+  constexpr int PER = (kMaxSplits + NSG - 1) / NSG;
+  const int c4 = tid % C4, sg = tid / C4;
+  float4 raw[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t s = sg + i * NSG;
+    raw[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (s < nsplit) {
+      const float* r = base + (size_t)s * REC + c4 * 4;
+      raw[i].x = ld_agent(r);
+      raw[i].y = ld_agent(r + 1);
+      raw[i].z = ld_agent(r + 2);
+      raw[i].w = ld_agent(r + 3);
+    }
+  }
   for (uint32_t s = tid; s < nsplit; s += NT) {
     s_sm[s] = ld_agent(base + (size_t)s * REC + D);
     s_sl[s] = ld_agent(base + (size_t)s * REC + D + 1);
@@ -338,18 +391,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   for (uint32_t s = 0; s < nsplit; ++s) mg = fmaxf(mg, s_sm[s]);
   float l = 0.f;
   for (uint32_t s = 0; s < nsplit; ++s) l += fast_exp2(s_sm[s] - mg) * s_sl[s];
-  constexpr int C4 = D / 4;
-  constexpr int NSG = NT / C4;
-  const int c4 = tid % C4, sg = tid / C4;
   float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (uint32_t s = sg; s < nsplit; s += NSG) {
-    const float f = fast_exp2(s_sm[s] - mg);
-    const float* r = base + (size_t)s * REC + c4 * 4;
-    a4.x += f * ld_agent(r);
-    a4.y += f * ld_agent(r + 1);
-    a4.z += f * ld_agent(r + 2);
-    a4.w += f * ld_agent(r + 3);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t s = sg + i * NSG;
+    if (s < nsplit) {
+      const float f = fast_exp2(s_sm[s] - mg);
+      a4.x += f * raw[i].x;
+      a4.y += f * raw[i].y;
+      a4.z += f * raw[i].z;
+      a4.w += f * raw[i].w;
+    }
   }
   st4(&s_red[sg * D + c4 * 4], a4);
   __syncthreads();
@@ -387,7 +439,7 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
     if (chunk == 0) chunk = kRpi;
     nsplit = 1;
   } else {
-    static const int target_mult = env_int("STS_DECODE_WG_PER_CU", 2);
+    static const int target_mult = env_int("STS_DECODE_WG_PER_CU", 1);
     static const int chunk_max = env_int("STS_DECODE_CHUNK_MAX", 512);
     static const int chunk_min = env_int("STS_DECODE_CHUNK_MIN", 64);
     const uint64_t target = (uint64_t)device_cu_count() * (uint64_t)target_mult;
@@ -408,7 +460,9 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   }
   p.chunk = chunk;
   p.nsplit_max = nsplit;
+  static const bool pipe = env_int("STS_DECODE_PIPE", 1) != 0;
   if (nsplit > 1) {
+    // Partials and arrival counters.
     Workspace* ws = nullptr;
     const int rc = get_workspace(stream, (size_t)units * nsplit * (head_dim + 4), units, &ws);
     if (rc != STS_OK) return rc;
@@ -420,14 +474,18 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   const dim3 grid(nsplit, p.H, batch);
   if (head_dim == 128) {
     if (waves == 1)
-      hipLaunchKernelGGL((decode_kernel<128, 1>), grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 1, false>), grid, dim3(64), 0, stream, p);
+    else if (pipe)
+      hipLaunchKernelGGL((decode_kernel<128, 4, true>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<128, 4>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 4, false>), grid, dim3(256), 0, stream, p);
   } else if (head_dim == 64) {
     if (waves == 1)
-      hipLaunchKernelGGL((decode_kernel<64, 1>), grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, 1, false>), grid, dim3(64), 0, stream, p);
+    else if (pipe)
+      hipLaunchKernelGGL((decode_kernel<64, 4, true>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<64, 4>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, 4, false>), grid, dim3(256), 0, stream, p);
   } else {
     return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
   }

@@ -44,17 +44,28 @@ template <int D, bool BF16>
 struct PrefillSmem {
   using T = typename std::conditional<BF16, __bf16, float>::type;
   static constexpr int KP = BF16 ? D + 8 : D + 4;  // K row pitch: 16 rows hit distinct banks
-  static constexpr int VP = kBK + 4;               // V^T row pitch
+  static constexpr int VP = 80;                    // V^T row pitch (keys), see vt_col
   alignas(16) T ks[kBK * KP];
   alignas(16) T vt[D * VP];
 };
+
+// V^T is stored d-major with the 4-key quads of each row permuted by
+// ((d >> 2) ^ (d >> 4)) & 15: with a 80-element pitch the staging writes
+// (32 lanes on 32 different rows) and the MFMA operand reads (16 rows x 4
+// quads) both hit 64 distinct banks.
+__device__ __forceinline__ int vt_col(int d, int quad) {
+  return 4 * (quad ^ (((d >> 2) ^ (d >> 4)) & 15));
+}
 
 template <int D, bool BF16>
 __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   using Smem = PrefillSmem<D, BF16>;
   constexpr int KP = Smem::KP;
   constexpr int VP = Smem::VP;
-  constexpr int DT = D / 16;  // O^T tiles of 16 dims
+  constexpr int DT = D / 16;         // O^T tiles of 16 dims
+  constexpr int C4 = D / 4;          // float4 columns of a row
+  constexpr int KPER = kBK * C4 / 256;        // K float4 per thread per block
+  constexpr int VQ = (kBK / 4) * C4 / 256;    // V 4-key x 4-dim squares per thread
   __shared__ Smem sm;
 
   const int tid = threadIdx.x;
@@ -69,6 +80,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   const uint32_t qi = qt * kBQ + wave * 16 + l16;
   const bool q_ok = qi < p.S;
   const uint32_t w_q = base_w + qi;  // window row of this lane's query
+  // Last window row any query of this wave can see (blocks beyond it are skipped).
+  const uint32_t w_wave = base_w + min(p.S - 1, qt * kBQ + wave * 16 + 15);
 
   // B operand of S^T = K Q^T: this lane's query row, permuted per MFMA.
   constexpr int QN = BF16 ? D / 32 : D / 16;
@@ -103,19 +116,33 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   const uint32_t kend = min(p.len, base_w + q_last + 1);  // keys this workgroup needs
   const float* kh = p.k + (size_t)h * p.M * D;
   const float* vh = p.v + (size_t)h * p.M * D;
+  const int d4 = tid % C4;
 
-  for (uint32_t kb = 0; kb < kend; kb += kBK) {
-    __syncthreads();  // the previous block's LDS reads are done
-    // K block -> ks[key][d]
-    for (int i = tid; i < kBK * D / 4; i += 256) {
-      const int key = i / (D / 4), d4 = i % (D / 4);
-      const uint32_t r = kb + key;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < kend) {
-        uint32_t slot = p.start + r;
-        slot = slot >= p.M ? slot - p.M : slot;
-        x = ld4(kh + (size_t)slot * D + d4 * 4);
-      }
+  // Next block's K and V rows, in flight while the current block computes.
+  // Rows past kend re-read row kend-1 (finite, and masked out of the softmax).
+  float4 kreg[KPER];
+  float4 vreg[VQ][4];
+  auto row_ptr = [&](const float* base, uint32_t r) {
+    r = r < kend ? r : kend - 1;
+    uint32_t slot = p.start + r;
+    slot = slot >= p.M ? slot - p.M : slot;
+    return base + (size_t)slot * D + d4 * 4;
+  };
+  auto prefetch = [&](uint32_t kb) {
+#pragma unroll
+    for (int i = 0; i < KPER; ++i) kreg[i] = ld4(row_ptr(kh, kb + tid / C4 + i * (256 / C4)));
+#pragma unroll
+    for (int i = 0; i < VQ; ++i) {
+      const int kq = tid / C4 + i * (256 / C4);
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) vreg[i][r4] = ld4(row_ptr(vh, kb + kq * 4 + r4));
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < KPER; ++i) {
+      const int key = tid / C4 + i * (256 / C4);
+      const float4 x = kreg[i];
       if constexpr (BF16) {
         bf16x4 y;
         y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
@@ -124,45 +151,35 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
         *reinterpret_cast<float4*>(&sm.ks[key * KP + d4 * 4]) = x;
       }
     }
-    // V block -> vt[d][key]; a thread moves a 4-key x 4-dim square
-    for (int i = tid; i < (kBK / 4) * (D / 4); i += 256) {
-      const int d4 = i % (D / 4), kq = i / (D / 4);
-      float4 x[4];
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const uint32_t r = kb + kq * 4 + r4;
-        x[r4] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < kend) {
-          uint32_t slot = p.start + r;
-          slot = slot >= p.M ? slot - p.M : slot;
-          x[r4] = ld4(vh + (size_t)slot * D + d4 * 4);
-        }
-      }
-      if constexpr (BF16) {
-        bf16x4 c0, c1, c2, c3;
+    for (int i = 0; i < VQ; ++i) {
+      const int kq = tid / C4 + i * (256 / C4);
+      const float4* x = vreg[i];
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          c0[r4] = (__bf16)x[r4].x;
-          c1[r4] = (__bf16)x[r4].y;
-          c2[r4] = (__bf16)x[r4].z;
-          c3[r4] = (__bf16)x[r4].w;
+      for (int c = 0; c < 4; ++c) {
+        const int d = d4 * 4 + c;
+        const float e0 = c == 0 ? x[0].x : c == 1 ? x[0].y : c == 2 ? x[0].z : x[0].w;
+        const float e1 = c == 0 ? x[1].x : c == 1 ? x[1].y : c == 2 ? x[1].z : x[1].w;
+        const float e2 = c == 0 ? x[2].x : c == 1 ? x[2].y : c == 2 ? x[2].z : x[2].w;
+        const float e3 = c == 0 ? x[3].x : c == 1 ? x[3].y : c == 2 ? x[3].z : x[3].w;
+        if constexpr (BF16) {
+          bf16x4 y;
+          y[0] = (__bf16)e0; y[1] = (__bf16)e1; y[2] = (__bf16)e2; y[3] = (__bf16)e3;
+          *reinterpret_cast<bf16x4*>(&sm.vt[d * VP + vt_col(d, kq)]) = y;
+        } else {
+          *reinterpret_cast<float4*>(&sm.vt[d * VP + vt_col(d, kq)]) = make_float4(e0, e1, e2, e3);
         }
-        *reinterpret_cast<bf16x4*>(&sm.vt[(d4 * 4 + 0) * VP + kq * 4]) = c0;
-        *reinterpret_cast<bf16x4*>(&sm.vt[(d4 * 4 + 1) * VP + kq * 4]) = c1;
-        *reinterpret_cast<bf16x4*>(&sm.vt[(d4 * 4 + 2) * VP + kq * 4]) = c2;
-        *reinterpret_cast<bf16x4*>(&sm.vt[(d4 * 4 + 3) * VP + kq * 4]) = c3;
-      } else {
-        *reinterpret_cast<float4*>(&sm.vt[(d4 * 4 + 0) * VP + kq * 4]) =
-            make_float4(x[0].x, x[1].x, x[2].x, x[3].x);
-        *reinterpret_cast<float4*>(&sm.vt[(d4 * 4 + 1) * VP + kq * 4]) =
-            make_float4(x[0].y, x[1].y, x[2].y, x[3].y);
-        *reinterpret_cast<float4*>(&sm.vt[(d4 * 4 + 2) * VP + kq * 4]) =
-            make_float4(x[0].z, x[1].z, x[2].z, x[3].z);
-        *reinterpret_cast<float4*>(&sm.vt[(d4 * 4 + 3) * VP + kq * 4]) =
-            make_float4(x[0].w, x[1].w, x[2].w, x[3].w);
       }
     }
+  };
+
+  prefetch(0);
+  for (uint32_t kb = 0; kb < kend; kb += kBK) {
+    __syncthreads();  // the previous block's LDS reads are done
+    stage();
     __syncthreads();
+    if (kb + kBK < kend) prefetch(kb + kBK);
+    if (kb > w_wave) continue;  // every key of this block is masked for this wave
 
     // S^T tiles t: keys kb + 16t + 4g + j, query qi.
     floatx4 s[4];
@@ -230,9 +247,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const __bf16* row = &sm.vt[(16 * t + l16) * VP + 32 * kk + 4 * g];
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16);
+          const int d = 16 * t + l16;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, 8 * kk + g)]);
+          const bf16x4 hi =
+              *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, 8 * kk + 4 + g)]);
           bf16x8 vop;
           vop[0] = lo[0]; vop[1] = lo[1]; vop[2] = lo[2]; vop[3] = lo[3];
           vop[4] = hi[0]; vop[5] = hi[1]; vop[6] = hi[2]; vop[7] = hi[3];
@@ -244,8 +262,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int tk = 0; tk < 4; ++tk) {
-          const float4 vf =
-              *reinterpret_cast<const float4*>(&sm.vt[(16 * t + l16) * VP + 16 * tk + 4 * g]);
+          const int d = 16 * t + l16;
+          const float4 vf = *reinterpret_cast<const float4*>(&sm.vt[d * VP + vt_col(d, 4 * tk + g)]);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[tk][0], o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[tk][1], o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[tk][2], o[t], 0, 0, 0);
