@@ -29,6 +29,7 @@ BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
 FP32_PEAK_TFLOPS = 157.3       # fp32 MFMA
 
 LAYERS, H, D, M = 24, 32, 128, 3000
+CALIB_BYTES = 256 << 20
 
 
 def parse():
@@ -38,6 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="", help="comma list of sections to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (counter calibration)")
     return ap.parse_args()
 
 
@@ -173,10 +176,22 @@ def bench_depformer(torch, sts, stream, steps, warmup):
     with Timer(torch, stream) as t:
         for _ in range(steps):
             frame()
-    us_frame = t.ms * 1e3 / steps
+    us_eager = t.ms * 1e3 / steps
+    # The frame recorded once as a HIP graph (what a serving loop does): the
+    # 48 launches replay without per-launch host cost.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        frame()
+    for _ in range(warmup):
+        graph.replay()
+    with Timer(torch, stream) as tg:
+        for _ in range(steps):
+            graph.replay()
+    us_frame = tg.ms * 1e3 / steps
     kv_bytes = sum(2 * B * Hd * (s + 1) * Dd * 4 for s in range(nsteps)) * layers
     return {"us_per_frame": us_frame, "launches_per_frame": nsteps * layers,
             "us_per_launch": us_frame / (nsteps * layers),
+            "eager_us_per_frame": us_eager,
             "kv_read_gbs": kv_bytes / (us_frame * 1e-6) / 1e9}
 
 
@@ -269,6 +284,15 @@ def main():
     stream = torch.cuda.Stream()
     extra = {}
     with torch.cuda.stream(stream):
+        if args.calib_copy:
+            # A copy of known size: 256 MiB read + 256 MiB written, used to scale
+            # the FETCH_SIZE / WRITE_SIZE counters of the kernels below.
+            src = torch.ones(CALIB_BYTES // 4, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
         log("bench: decode (config 2)")
         dec = bench_decode(torch, sts, stream, args.steps, args.warmup)
         if want("prefill"):

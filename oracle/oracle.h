@@ -6,9 +6,10 @@
  * as the timed CPU baseline -- never as a product path.
  *
  * Every function cites the reference file:line it restates (paths relative to
- * crates/sts-wasm/src/ of idle-intelligence/sts-web).  How each one is pinned
- * (closed forms, library routines, reference unit tests) is listed in
- * oracle/README.md.
+ * crates/sts-wasm/src/ of idle-intelligence/sts-web).  tests/test_oracle.py
+ * pins each one against something independent of this code: closed forms,
+ * scipy/torch routines, the reference's own KVCache unit-test sequences,
+ * brute force on tiny inputs, and planted mistakes that must be caught.
  */
 #ifndef STS_ORACLE_H
 #define STS_ORACLE_H
