@@ -4,21 +4,28 @@
 // softmax((Q K^T) * scale + mask) V with key j masked when j > offset + i
 // (apply_causal_mask, model.rs:539-563), here over a ring window that may wrap.
 //
-// One workgroup = one head x 64 queries (16 per wave); keys stream through LDS
-// in blocks of 64.  Each wave computes S^T = K Q^T for its 16 queries, so that
-// the accumulator layout of S^T (lane l: keys 4*(l/16)+j of each 16-key tile,
-// query l%16) is, after the online softmax, directly the B operand P^T of
-// O^T = V^T P^T.  The contraction order over keys is permuted identically in
-// V^T and P^T, so P never goes through LDS.  Each query's max and sum are
-// reduced over the 4 lanes {l%16 + 16g} that hold its keys.
+// One workgroup = one head x 64 queries; keys stream through LDS in blocks of
+// 64.  Eight waves: wave w owns queries 16*(w%4)..+15 and key slice w/4 (32
+// keys) of every block, with its own online softmax; the two slices of a
+// query group merge through LDS at the end.  Each wave computes S^T = K Q^T,
+// so that the accumulator layout of S^T (lane l: keys 4*(l/16)+j of each
+// 16-key tile, query l%16) is, after the online softmax, directly the B
+// operand P^T of O^T = V^T P^T.  The contraction order over keys is permuted
+// identically in V^T and P^T, so P never goes through LDS.  Each query's max
+// and sum are reduced over the 4 lanes {l%16 + 16g} that hold its keys.
 //
-//   BF16 = true : f32 K/V/Q rounded to bf16 while staging, v_mfma_f32_16x16x32_bf16,
-//                 f32 softmax and accumulation.
+//   BF16 = true : f32 K/V/Q rounded to bf16 while staging, v_mfma_f32_16x16x32_bf16
+//                 (16x16x16 for 16-key slices), f32 softmax and accumulation.
 //   BF16 = false: f32 throughout, v_mfma_f32_16x16x4f32.
 //
-// Blocks are indexed (head, q-tile) with head fastest, so all q-tiles of a
-// head land on the same XCD (workgroup id % 8) and share its L2 copy of the
-// head's K/V; the heaviest (last) q-tiles are dispatched first.
+// The f32 variant also splits each tile's key range over up to four
+// workgroups (blockIdx.z); each publishes (O, max, sum) with device-coherent
+// stores and the last to arrive folds them in split order.
+//
+// Blocks are indexed (head, q-tile, split) with head fastest, so all
+// workgroups of a head land on the same XCD (workgroup id % 8) and share its
+// L2 copy of the head's K/V; the heaviest (last) q-tiles are dispatched first.
+#include <algorithm>
 #include <cfloat>
 #include <type_traits>
 
@@ -33,12 +40,17 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;  // queries per workgroup
 constexpr int kBK = 64;  // keys per LDS block
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 scale4(float4 x, float c) {
+  return make_float4(x.x * c, x.y * c, x.z * c, x.w * c);
+}
 
 template <int D, bool BF16>
 struct PrefillSmem {
@@ -49,6 +61,15 @@ struct PrefillSmem {
   alignas(16) T vt[D * VP];
 };
 
+constexpr int kMaxPrefillSplits = 4;
+constexpr int kKsplit = 2;  // waves per query group (key slices of a block)
+
+// Split partials cross workgroups (and XCDs, each with its own L2) through
+// buffer loads and stores with the sc1 cache policy (device coherence), 16
+// bytes per lane so that every store fills whole 64-byte segments.
+constexpr int kSc1 = 16;                        // cache-policy bit of sc1
+constexpr int kBufferWord3 = 0x00020000;        // raw 32-bit buffer, no swizzle
+
 // V^T is stored d-major with the 4-key quads of each row permuted by
 // ((d >> 2) ^ (d >> 4)) & 15: with a 80-element pitch the staging writes
 // (32 lanes on 32 different rows) and the MFMA operand reads (16 rows x 4
@@ -57,31 +78,46 @@ __device__ __forceinline__ int vt_col(int d, int quad) {
   return 4 * (quad ^ (((d >> 2) ^ (d >> 4)) & 15));
 }
 
-template <int D, bool BF16>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
+// KSPLIT waves share each group of 16 queries: wave w handles queries
+// 16 * (w % 4) .. +15 of the tile and the key slice w / 4 (64 / KSPLIT keys)
+// of every 64-key block, with its own online softmax; the slices merge once
+// at the end.  More waves per SIMD hide the latency of each wave's serial
+// softmax/MFMA chain.
+template <int D, bool BF16, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillParams p) {
   using Smem = PrefillSmem<D, BF16>;
+  constexpr int NT = 256 * KSPLIT;
   constexpr int KP = Smem::KP;
   constexpr int VP = Smem::VP;
-  constexpr int DT = D / 16;         // O^T tiles of 16 dims
-  constexpr int C4 = D / 4;          // float4 columns of a row
-  constexpr int KPER = kBK * C4 / 256;        // K float4 per thread per block
-  constexpr int VQ = (kBK / 4) * C4 / 256;    // V 4-key x 4-dim squares per thread
+  constexpr int DT = D / 16;           // O^T tiles of 16 dims
+  constexpr int C4 = D / 4;            // float4 columns of a row
+  constexpr int KW = kBK / KSPLIT;     // keys per wave per block
+  constexpr int TW = KW / 16;          // S^T tiles per wave per block
+  constexpr int KPER = kBK * C4 / NT;  // K float4 per thread per block
+  constexpr int VSQ = (kBK / 4) * C4;  // V 4-key x 4-dim squares per block
+  constexpr int VPER = VSQ >= NT ? VSQ / NT : 1;
+  static_assert(KPER >= 1 && TW >= 1, "tile shape");
   __shared__ Smem sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int qg = wave & 3;       // query group
+  const int kslice = wave >> 2;  // key slice
   const int g = lane >> 4;
   const int l16 = lane & 15;
   const uint32_t h = blockIdx.x;
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   const uint32_t qt = nqt - 1 - blockIdx.y;
+  const uint32_t split = blockIdx.z;
   const uint32_t base_w = p.len - p.S;
-  const uint32_t qi = qt * kBQ + wave * 16 + l16;
+  const uint32_t qi = qt * kBQ + qg * 16 + l16;
   const bool q_ok = qi < p.S;
   const uint32_t w_q = base_w + qi;  // window row of this lane's query
-  // Last window row any query of this wave can see (blocks beyond it are skipped).
-  const uint32_t w_wave = base_w + min(p.S - 1, qt * kBQ + wave * 16 + 15);
+  // Window rows of the first and last query of this wave: keys up to w_first
+  // need no causal mask, keys past w_wave are skipped.
+  const uint32_t w_first = base_w + qt * kBQ + qg * 16;
+  const uint32_t w_wave = base_w + min(p.S - 1, qt * kBQ + qg * 16 + 15);
 
   // B operand of S^T = K Q^T: this lane's query row, permuted per MFMA.
   constexpr int QN = BF16 ? D / 32 : D / 16;
@@ -93,8 +129,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       // dims 32a + 8g .. +7
       float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
       if (q_ok) {
-        x0 = ld4(qrow + a * 32 + g * 8);
-        x1 = ld4(qrow + a * 32 + g * 8 + 4);
+        x0 = scale4(ld4(qrow + a * 32 + g * 8), p.scale_log2);
+        x1 = scale4(ld4(qrow + a * 32 + g * 8 + 4), p.scale_log2);
       }
       bf16x8 b;
       b[0] = (__bf16)x0.x; b[1] = (__bf16)x0.y; b[2] = (__bf16)x0.z; b[3] = (__bf16)x0.w;
@@ -102,7 +138,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       qop[a] = b;
     } else {
       // dims 16a + 4g .. +3 (instruction (a, j) contracts dim 16a + 4g + j)
-      qop[a] = q_ok ? ld4(qrow + a * 16 + g * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qop[a] = q_ok ? scale4(ld4(qrow + a * 16 + g * 4), p.scale_log2)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
 
@@ -113,88 +150,138 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   for (int t = 0; t < DT; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t q_last = min(p.S, (qt + 1) * kBQ) - 1;
-  const uint32_t kend = min(p.len, base_w + q_last + 1);  // keys this workgroup needs
-  const float* kh = p.k + (size_t)h * p.M * D;
-  const float* vh = p.v + (size_t)h * p.M * D;
+  const uint32_t kend = min(p.len, base_w + q_last + 1);  // keys this query tile needs
+  // This workgroup's share of the tile's key blocks (sizes differ by at most one).
+  const uint32_t nb = (kend + kBK - 1) / kBK;
+  const uint32_t ns = min(p.nsplit, nb);
+  if (split >= ns) return;  // the tile has fewer blocks than splits
+  const uint32_t kb_begin = split * nb / ns * kBK;
+  const uint32_t kb_end = min(kend, (split + 1) * nb / ns * kBK);
   const int d4 = tid % C4;
 
-  // Next block's K and V rows, in flight while the current block computes.
-  // Rows past kend re-read row kend-1 (finite, and masked out of the softmax).
-  float4 kreg[KPER];
-  float4 vreg[VQ][4];
-  auto row_ptr = [&](const float* base, uint32_t r) {
-    r = r < kend ? r : kend - 1;
-    uint32_t slot = p.start + r;
-    slot = slot >= p.M ? slot - p.M : slot;
-    return base + (size_t)slot * D + d4 * 4;
+  // K/V rows come in through buffer loads on per-head resources (byte offset
+  // slot * D * 4 + column).  A block whose 64 rows are all inside the window
+  // and do not wrap needs no per-row arithmetic: per-thread constant offsets
+  // plus one scalar block offset.  Other blocks compute each row's slot; rows
+  // past the tile's last key get an offset past the resource, which loads
+  // zeros (finite, and masked out of the softmax).
+  constexpr uint32_t ROWB = D * sizeof(float);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.k) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.v) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+  const bool v_thread = VSQ >= NT || tid < VSQ;
+  auto k_row = [&](int i) { return (uint32_t)(tid / C4 + i * (NT / C4)); };
+  auto v_row = [&](int i, int r4) { return (uint32_t)((tid / C4 + i * (NT / C4)) * 4 + r4); };
+
+  struct Buf {
+    floatx4 k[KPER];
+    floatx4 v[VPER][4];
   };
-  auto prefetch = [&](uint32_t kb) {
+  Buf buf;
+  // Loads block kb into b; valid == false loads zeros (keeps the number of
+  // loads in flight the same on every path).  Only the offsets depend on the
+  // path; the loads themselves are issued unconditionally, so the compiler's
+  // wait counts see one fixed order of loads.
+  constexpr int NL = KPER + 4 * VPER;
+  auto fetch = [&](Buf& b, uint32_t kb, bool valid) {
+    uint32_t slot0 = p.start + kb;
+    slot0 = slot0 >= p.M ? slot0 - p.M : slot0;
+    uint32_t vo[NL];
+    uint32_t so = 0;
+    if (valid && kb + kBK <= kend && slot0 + kBK <= p.M) {
+      so = slot0 * ROWB;
 #pragma unroll
-    for (int i = 0; i < KPER; ++i) kreg[i] = ld4(row_ptr(kh, kb + tid / C4 + i * (256 / C4)));
+      for (int i = 0; i < KPER; ++i) vo[i] = k_row(i) * ROWB + d4 * 16;
 #pragma unroll
-    for (int i = 0; i < VQ; ++i) {
-      const int kq = tid / C4 + i * (256 / C4);
+      for (int i = 0; i < VPER; ++i)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) vreg[i][r4] = ld4(row_ptr(vh, kb + kq * 4 + r4));
+        for (int r4 = 0; r4 < 4; ++r4) vo[KPER + 4 * i + r4] = v_row(i, r4) * ROWB + d4 * 16;
+    } else {
+      const uint32_t lim = valid ? kend : 0u;
+      auto off = [&](uint32_t r) {
+        const uint32_t row = kb + r;
+        uint32_t slot = slot0 + r;
+        slot = min(slot, slot - p.M);  // wrap (slot < 2M)
+        return row < lim ? slot * ROWB + d4 * 16 : 0xFFFFFFF0u;
+      };
+#pragma unroll
+      for (int i = 0; i < KPER; ++i) vo[i] = off(k_row(i));
+#pragma unroll
+      for (int i = 0; i < VPER; ++i)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) vo[KPER + 4 * i + r4] = off(v_row(i, r4));
+    }
+#pragma unroll
+    for (int i = 0; i < KPER; ++i)
+      b.k[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo[i], so, 0));
+    if (v_thread) {
+#pragma unroll
+      for (int i = 0; i < VPER; ++i)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          b.v[i][r4] = __builtin_bit_cast(
+              floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo[KPER + 4 * i + r4], so, 0));
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](const Buf& b) {
 #pragma unroll
     for (int i = 0; i < KPER; ++i) {
-      const int key = tid / C4 + i * (256 / C4);
-      const float4 x = kreg[i];
+      const int key = tid / C4 + i * (NT / C4);
+      const floatx4 x = b.k[i];
       if constexpr (BF16) {
         bf16x4 y;
         y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
         *reinterpret_cast<bf16x4*>(&sm.ks[key * KP + d4 * 4]) = y;
       } else {
-        *reinterpret_cast<float4*>(&sm.ks[key * KP + d4 * 4]) = x;
+        *reinterpret_cast<floatx4*>(&sm.ks[key * KP + d4 * 4]) = x;
       }
     }
+    if (v_thread) {
 #pragma unroll
-    for (int i = 0; i < VQ; ++i) {
-      const int kq = tid / C4 + i * (256 / C4);
-      const float4* x = vreg[i];
+      for (int i = 0; i < VPER; ++i) {
+        const int kq = tid / C4 + i * (NT / C4);
+        const floatx4* x = b.v[i];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = d4 * 4 + c;
-        const float e0 = c == 0 ? x[0].x : c == 1 ? x[0].y : c == 2 ? x[0].z : x[0].w;
-        const float e1 = c == 0 ? x[1].x : c == 1 ? x[1].y : c == 2 ? x[1].z : x[1].w;
-        const float e2 = c == 0 ? x[2].x : c == 1 ? x[2].y : c == 2 ? x[2].z : x[2].w;
-        const float e3 = c == 0 ? x[3].x : c == 1 ? x[3].y : c == 2 ? x[3].z : x[3].w;
-        if constexpr (BF16) {
-          bf16x4 y;
-          y[0] = (__bf16)e0; y[1] = (__bf16)e1; y[2] = (__bf16)e2; y[3] = (__bf16)e3;
-          *reinterpret_cast<bf16x4*>(&sm.vt[d * VP + vt_col(d, kq)]) = y;
-        } else {
-          *reinterpret_cast<float4*>(&sm.vt[d * VP + vt_col(d, kq)]) = make_float4(e0, e1, e2, e3);
+        for (int c = 0; c < 4; ++c) {
+          const int d = d4 * 4 + c;
+          const float e0 = c == 0 ? x[0].x : c == 1 ? x[0].y : c == 2 ? x[0].z : x[0].w;
+          const float e1 = c == 0 ? x[1].x : c == 1 ? x[1].y : c == 2 ? x[1].z : x[1].w;
+          const float e2 = c == 0 ? x[2].x : c == 1 ? x[2].y : c == 2 ? x[2].z : x[2].w;
+          const float e3 = c == 0 ? x[3].x : c == 1 ? x[3].y : c == 2 ? x[3].z : x[3].w;
+          if constexpr (BF16) {
+            bf16x4 y;
+            y[0] = (__bf16)e0; y[1] = (__bf16)e1; y[2] = (__bf16)e2; y[3] = (__bf16)e3;
+            *reinterpret_cast<bf16x4*>(&sm.vt[d * VP + vt_col(d, kq)]) = y;
+          } else {
+            *reinterpret_cast<float4*>(&sm.vt[d * VP + vt_col(d, kq)]) =
+                make_float4(e0, e1, e2, e3);
+          }
         }
       }
     }
   };
 
-  prefetch(0);
-  for (uint32_t kb = 0; kb < kend; kb += kBK) {
-    __syncthreads();  // the previous block's LDS reads are done
-    stage();
-    __syncthreads();
-    if (kb + kBK < kend) prefetch(kb + kBK);
-    if (kb > w_wave) continue;  // every key of this block is masked for this wave
+  const uint32_t nblk = (kb_end - kb_begin + kBK - 1) / kBK;
+  // One block out of LDS: S^T, online softmax, O^T update.
+  auto compute = [&](uint32_t kb) {
+    const uint32_t k0 = kb + kslice * KW;  // first key of this wave's slice
+    if (k0 > w_wave) return;               // every key of the slice is masked for this wave
+    const bool unmasked = k0 + KW <= kend && k0 + KW - 1 <= w_first;
 
-    // S^T tiles t: keys kb + 16t + 4g + j, query qi.
-    floatx4 s[4];
+    // S^T tiles t: keys k0 + 16t + 4g + j, query qi.
+    floatx4 s[TW];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TW; ++t) {
+      const int krow = kslice * KW + 16 * t + l16;
       s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int a = 0; a < QN; ++a) {
         if constexpr (BF16) {
-          const bf16x8 kop =
-              *reinterpret_cast<const bf16x8*>(&sm.ks[(16 * t + l16) * KP + a * 32 + g * 8]);
+          const bf16x8 kop = *reinterpret_cast<const bf16x8*>(&sm.ks[krow * KP + a * 32 + g * 8]);
           s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[a], s[t], 0, 0, 0);
         } else {
-          const float4 kf =
-              *reinterpret_cast<const float4*>(&sm.ks[(16 * t + l16) * KP + a * 16 + g * 4]);
+          const float4 kf = *reinterpret_cast<const float4*>(&sm.ks[krow * KP + a * 16 + g * 4]);
           s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qop[a].x, s[t], 0, 0, 0);
           s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qop[a].y, s[t], 0, 0, 0);
           s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qop[a].z, s[t], 0, 0, 0);
@@ -203,18 +290,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       }
     }
 
-    // Causal mask and online softmax for query qi over this block.
+    // Causal mask and online softmax for query qi over this slice (q carries
+    // the scale, so scores are already in log2 units).
     float mx = -INFINITY;
+    if (unmasked) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < TW; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t key = kb + 16 * t + 4 * g + j;
-        float x = s[t][j] * p.scale_log2;
-        x = (key <= w_q && key < kend) ? x : -INFINITY;
-        s[t][j] = x;
-        mx = fmaxf(mx, x);
-      }
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[t][j]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < TW; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t key = k0 + 16 * t + 4 * g + j;
+          const float x = (key <= w_q && key < kend) ? s[t][j] : -INFINITY;
+          s[t][j] = x;
+          mx = fmaxf(mx, x);
+        }
+    }
     mx = fmaxf(mx, swizzle_xor16(mx));
     mx = fmaxf(mx, xor32(mx));
     const float mn = fmaxf(m, mx);
@@ -222,7 +316,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
     m = mn;
     float ps = 0.f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < TW; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float e = fast_exp2(s[t][j] - mn);
@@ -232,65 +326,248 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
     ps += swizzle_xor16(ps);
     ps += xor32(ps);
     lsum = lsum * alpha + ps;
+    // Rescale only when some lane's running max moved (alpha == 1 otherwise).
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T over this wave's KW keys.
+    const int q0 = kslice * (KW / 4);  // first 4-key quad of the slice
     if constexpr (BF16) {
+      if constexpr (KW >= 32) {
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        bf16x8 pb;
+        for (int kk = 0; kk < KW / 32; ++kk) {
+          bf16x8 pb;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pb[j] = (__bf16)s[2 * kk][j];
-          pb[4 + j] = (__bf16)s[2 * kk + 1][j];
+          for (int j = 0; j < 4; ++j) {
+            pb[j] = (__bf16)s[2 * kk][j];
+            pb[4 + j] = (__bf16)s[2 * kk + 1][j];
+          }
+#pragma unroll
+          for (int t = 0; t < DT; ++t) {
+            const int d = 16 * t + l16;
+            const bf16x4 lo =
+                *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 8 * kk + g)]);
+            const bf16x4 hi =
+                *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 8 * kk + 4 + g)]);
+            bf16x8 vop;
+            vop[0] = lo[0]; vop[1] = lo[1]; vop[2] = lo[2]; vop[3] = lo[3];
+            vop[4] = hi[0]; vop[5] = hi[1]; vop[6] = hi[2]; vop[7] = hi[3];
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pb, o[t], 0, 0, 0);
+          }
         }
+      } else {
+        // 16 keys: the S^T tile's lane layout (keys 4g..4g+3) is the B operand
+        // of the 16x16x16 product directly.
+        bf16x4 pb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pb[j] = (__bf16)s[0][j];
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
           const int d = 16 * t + l16;
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, 8 * kk + g)]);
-          const bf16x4 hi =
-              *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, 8 * kk + 4 + g)]);
-          bf16x8 vop;
-          vop[0] = lo[0]; vop[1] = lo[1]; vop[2] = lo[2]; vop[3] = lo[3];
-          vop[4] = hi[0]; vop[5] = hi[1]; vop[6] = hi[2]; vop[7] = hi[3];
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pb, o[t], 0, 0, 0);
+          const bf16x4 vop = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + g)]);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vop),
+                                                          __builtin_bit_cast(s16x4, pb), o[t], 0,
+                                                          0, 0);
         }
       }
     } else {
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
+        for (int tk = 0; tk < TW; ++tk) {
           const int d = 16 * t + l16;
-          const float4 vf = *reinterpret_cast<const float4*>(&sm.vt[d * VP + vt_col(d, 4 * tk + g)]);
+          const float4 vf =
+              *reinterpret_cast<const float4*>(&sm.vt[d * VP + vt_col(d, q0 + 4 * tk + g)]);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[tk][0], o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[tk][1], o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[tk][2], o[t], 0, 0, 0);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, s[tk][3], o[t], 0, 0, 0);
         }
     }
+  };
+
+  // One block in flight in registers while the previous one computes.
+  fetch(buf, kb_begin, true);
+  for (uint32_t i = 0; i < nblk; ++i) {
+    const uint32_t kb = kb_begin + i * kBK;
+    __syncthreads();  // the previous block's LDS reads are done
+    stage(buf);
+    __syncthreads();
+    fetch(buf, min(kb + kBK, kb_begin + (nblk - 1) * kBK), i + 1 < nblk);
+    compute(kb);
   }
 
-  if (q_ok) {
-    float* orow = p.out + ((size_t)qi * p.H + h) * D;
+  // Merge the key slices of each query group: slice r > 0 parks (m, l, O^T)
+  // in LDS (reusing the K/V tiles), slice 0 folds it in; one round per slice.
+  if constexpr (KSPLIT > 1) {
+    float* red = reinterpret_cast<float*>(&sm);  // [4 groups][64 lanes][DT*4 + 2]
+    constexpr int RS = DT * 4 + 2;
+    static_assert(4 * 64 * RS * sizeof(float) <= sizeof(Smem), "merge scratch");
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      float4 r;
-      r.x = o[t][0] / lsum;
-      r.y = o[t][1] / lsum;
-      r.z = o[t][2] / lsum;
-      r.w = o[t][3] / lsum;
-      *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) = r;
+    for (int r = 1; r < KSPLIT; ++r) {
+      __syncthreads();
+      if (kslice == r) {
+        float* dst = red + (qg * 64 + lane) * RS;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dst[4 * t + j] = o[t][j];
+        dst[DT * 4] = m;
+        dst[DT * 4 + 1] = lsum;
+      }
+      __syncthreads();
+      if (kslice == 0) {
+        const float* src = red + (qg * 64 + lane) * RS;
+        const float m2 = src[DT * 4], l2 = src[DT * 4 + 1];
+        const float mm = fmaxf(m, m2);
+        const float f1 = fast_exp2(m - mm), f2 = fast_exp2(m2 - mm);
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[t][j] = o[t][j] * f1 + src[4 * t + j] * f2;
+        lsum = lsum * f1 + l2 * f2;
+        m = mm;
+      }
     }
   }
+  // From here on, the waves of key slice 0 hold each query group's result.
+  const bool owner = kslice == 0;
+  float* orow = p.out + ((size_t)qi * p.H + h) * D;
+
+  if (ns == 1) {
+    if (owner && q_ok) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        float4 r;
+        r.x = o[t][0] / lsum;
+        r.y = o[t][1] / lsum;
+        r.z = o[t][2] / lsum;
+        r.w = o[t][3] / lsum;
+        *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) = r;
+      }
+    }
+    return;
+  }
+
+  // Publish this split's partial with device-coherent stores (the splits of a
+  // tile may run on different XCDs), wait for their acknowledgement, then take
+  // an arrival ticket.  Record layout: O as [t][group][lane] float4, then the
+  // running max and sum as [group][lane].
+  constexpr int REC = 256 * (DT * 4 + 2);
+  const size_t tile = (size_t)h * nqt + qt;
+  float* rec_tile = p.part + tile * p.nsplit * REC;
+  const int slot = qg * 64 + lane;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      rec_tile, 0, (int)(ns * REC * sizeof(float)), kBufferWord3);
+  if (owner) {
+    const uint32_t rec = split * REC * sizeof(float);
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[t]), rsrc,
+                                             rec + (t * 256 + slot) * 16, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m), rsrc,
+                                          rec + (DT * 4 * 256 + slot) * 4, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lsum), rsrc,
+                                          rec + (DT * 4 * 256 + 256 + slot) * 4, 0, kSc1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __shared__ uint32_t s_ticket;
+  uint32_t* ctr = p.counters + tile;
+  __syncthreads();
+  if (tid == 0) s_ticket = atomicAdd(ctr, 1u);
+  __syncthreads();
+  if (s_ticket != ns - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+  // Last to arrive: fold the splits in split order (whichever arrived last),
+  // so the result does not depend on arrival order.
+  if (owner) {
+    float ms[kMaxPrefillSplits], ls[kMaxPrefillSplits];
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxPrefillSplits; ++s2) {
+      ms[s2] = -FLT_MAX;
+      ls[s2] = 0.f;
+      if (s2 == (int)split) {
+        ms[s2] = m;
+        ls[s2] = lsum;
+      } else if (s2 < (int)ns) {
+        const uint32_t rec = s2 * REC * sizeof(float);
+        ms[s2] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, rec + (DT * 4 * 256 + slot) * 4, 0, kSc1));
+        ls[s2] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, rec + (DT * 4 * 256 + 256 + slot) * 4,
+                                                        0, kSc1));
+      }
+    }
+    float mm = ms[0];
+#pragma unroll
+    for (int s2 = 1; s2 < kMaxPrefillSplits; ++s2) mm = fmaxf(mm, ms[s2]);
+    float l = 0.f;
+    floatx4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxPrefillSplits; ++s2) {
+      if (s2 < (int)ns) {
+        const float f = fast_exp2(ms[s2] - mm);
+        l += f * ls[s2];
+        floatx4 os[DT];
+        if (s2 == (int)split) {
+#pragma unroll
+          for (int t = 0; t < DT; ++t) os[t] = o[t];
+        } else {
+          const uint32_t rec = s2 * REC * sizeof(float);
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+            os[t] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, rec + (t * 256 + slot) * 16, 0, kSc1));
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t) acc[t] += f * os[t];
+      }
+    }
+    if (q_ok) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        float4 r;
+        r.x = acc[t][0] / l;
+        r.y = acc[t][1] / l;
+        r.z = acc[t][2] / l;
+        r.w = acc[t][3] / l;
+        *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) = r;
+      }
+    }
+  }
+  if (tid == 0) atomicExch(ctr, 0u);
 }
 
 template <int D, bool BF16>
 int launch_t(const PrefillParams& p, hipStream_t stream) {
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
-  hipLaunchKernelGGL((prefill_kernel<D, BF16>), dim3(p.H, nqt), dim3(256), 0, stream, p);
+  if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
+    return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
+  // f32 tiles carry four times the MFMA work of bf16 ones: split their key
+  // ranges until there are about two workgroups per CU.  bf16 tiles are
+  // bound by the CU's load rate and gain nothing from splitting.
+  const uint32_t tiles = p.H * nqt;
+  const uint32_t cus = (uint32_t)device_cu_count();
+  uint32_t nsplit = BF16 ? 1u : (2 * cus + tiles - 1) / tiles;
+  nsplit = std::max(1u, std::min<uint32_t>(nsplit, kMaxPrefillSplits));
+  PrefillParams q = p;
+  q.nsplit = nsplit;
+  if (nsplit > 1) {
+    Workspace* ws = nullptr;
+    const int rc = get_workspace(stream, (size_t)tiles * nsplit * 256 * (D + 2), tiles, &ws);
+    if (rc != STS_OK) return rc;
+    q.part = ws->part;
+    q.counters = ws->counters;
+  }
+  hipLaunchKernelGGL((prefill_kernel<D, BF16, kKsplit>), dim3(p.H, nqt, nsplit),
+                     dim3(256 * kKsplit), 0, stream, q);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }

@@ -18,6 +18,12 @@ struct PrefillParams {
   uint32_t S = 0, H = 0, M = 0;
   uint32_t start = 0, len = 0;
   float scale_log2 = 0.f;
+  // Key-range split: up to nsplit workgroups share a (head, query tile); each
+  // publishes a partial (O, max, sum) to part and the last to arrive (counted
+  // in counters, one per (head, tile), left at zero) merges them.
+  uint32_t nsplit = 1;
+  float* part = nullptr;
+  uint32_t* counters = nullptr;
 };
 
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream);

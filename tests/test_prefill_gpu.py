@@ -54,6 +54,8 @@ def test_prefill_fixtures(gpu, name):
     (3, 64, 200, 17, 1, 190),         # single query == decode
     (2, 128, 1000, 100, 65, 950),     # ragged last q-tile
     (2, 64, 129, 64, 65, 100),        # chunk evicts nothing, wraps
+    (1, 128, 3000, 2000, 130, 5),     # few tiles: key range split four ways
+    (2, 64, 4096, 3000, 70, 4000),    # long wrapped window, split key range
 ])
 @pytest.mark.parametrize("prec", [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA])
 def test_prefill_against_f64(gpu, H, D, M, cached, S, start, prec):
@@ -101,3 +103,25 @@ def test_kv_prefill_appends_and_attends(gpu):
         np.testing.assert_array_equal(host(vb), vref)
         ref = oracle.prefill_f64(q, kref[0], vref[0], o.window_start(), o.len, scale_for(D))
         assert np.abs(got - ref).max() < TOL_F32, it
+
+
+@pytest.mark.parametrize("prec", [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA])
+def test_prefill_bit_repeatable_across_split_merges(gpu, prec):
+    """Split key ranges merge in split order whichever workgroup arrives last:
+    repeated launches, interleaved with split decodes that share the same
+    workspace and arrival counters, give identical bits."""
+    H, D, M, cached, S, start = 32, 128, 3000, 2000, 200, 2900
+    q, kc, vc = prefill_inputs(91, H, D, M, cached, S, start)
+    L = cached + S
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    first = host(sts_attn.prefill_attention(qd, kd, vd, start, L, scale_for(D), prec))
+    lens = torch.tensor([L], dtype=torch.int32, device="cuda")
+    st = torch.tensor([start], dtype=torch.int32, device="cuda")
+    dec0 = host(sts_attn.decode_ring(qd[-1][None], kd[None], vd[None], lens, st, scale_for(D)))
+    for rep in range(4):
+        dec = host(sts_attn.decode_ring(qd[-1][None], kd[None], vd[None], lens, st, scale_for(D)))
+        np.testing.assert_array_equal(dec, dec0)
+        got = host(sts_attn.prefill_attention(qd, kd, vd, start, L, scale_for(D), prec))
+        np.testing.assert_array_equal(got, first)
+    ref = oracle.prefill_f64(q, kc, vc, start, L, scale_for(D))
+    assert np.abs(first - ref).max() < (TOL_F32 if prec == sts_attn.PREC_F32 else TOL_BF16)
