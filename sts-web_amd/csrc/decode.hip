@@ -20,6 +20,7 @@
 #include <cfloat>
 
 #include "common.hpp"
+#include "coherent.hpp"
 #include "decode.hpp"
 #include "lane.hpp"
 
@@ -41,18 +42,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld4_stream(const float* p) {
   const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
   return make_float4(v.x, v.y, v.z, v.w);
-}
-
-// Split partials travel between workgroups (possibly on different XCDs, each
-// with its own L2) through accesses that carry device (agent) coherence scope
-// themselves -- global_store/global_load with sc1 -- so publishing them needs
-// only a wait for their acknowledgement, not an L2 write-back or invalidate
-// of everything the workgroup has touched.
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Interleaved RoPE of two adjacent pairs (model.rs:99-100), each product and
@@ -356,16 +345,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // hardware.
   constexpr int REC = D + 4;
   const size_t rec_base = ((size_t)b * p.H + h) * p.nsplit_max * REC;
-  float* rec = p.part + rec_base + (size_t)split * REC;
-  if (lane < C4) {
-    st_agent(rec + col * 4, a4.x);
-    st_agent(rec + col * 4 + 1, a4.y);
-    st_agent(rec + col * 4 + 2, a4.z);
-    st_agent(rec + col * 4 + 3, a4.w);
-  }
+  const __amdgpu_buffer_rsrc_t part_rs = coherent_rsrc(p.part + rec_base, p.nsplit_max * REC * 4);
+  const uint32_t rec = split * REC * 4;  // byte offset of this split's record
+  if (lane < C4) st_coherent4(part_rs, rec + col * 16, coh_f4{a4.x, a4.y, a4.z, a4.w});
   if (lane == 0) {
-    st_agent(rec + D, m_t);
-    st_agent(rec + D + 1, l_t);
+    st_coherent(part_rs, rec + D * 4, m_t);
+    st_coherent(part_rs, rec + D * 4 + 4, l_t);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -380,11 +365,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // column col of the splits grp, grp + NG2, ... in passes of kPass records,
   // all issued before the first use.
   constexpr int kPass = 4;
-  const float* base = p.part + rec_base;
   float ms = -FLT_MAX, ls = 0.f;
   if (lane < (int)nsplit) {
-    ms = ld_agent(base + (size_t)lane * REC + D);
-    ls = ld_agent(base + (size_t)lane * REC + D + 1);
+    ms = ld_coherent(part_rs, (lane * REC + D) * 4);
+    ls = ld_coherent(part_rs, (lane * REC + D + 1) * 4);
   }
   float4 raw[kPass];
   auto fetch = [&](uint32_t s0) {
@@ -393,8 +377,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       const uint32_t s = s0 + grp + NG2 * i;
       raw[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (s < nsplit) {
-        const float* r = base + (size_t)s * REC + col * 4;
-        raw[i] = make_float4(ld_agent(r), ld_agent(r + 1), ld_agent(r + 2), ld_agent(r + 3));
+        const coh_f4 x = ld_coherent4(part_rs, (s * REC + col * 4) * 4);
+        raw[i] = make_float4(x.x, x.y, x.z, x.w);
       }
     }
   };

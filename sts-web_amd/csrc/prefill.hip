@@ -29,6 +29,7 @@
 #include <cfloat>
 #include <type_traits>
 
+#include "coherent.hpp"
 #include "common.hpp"
 #include "lane.hpp"
 #include "prefill.hpp"
@@ -41,7 +42,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;  // queries per workgroup
 constexpr int kBK = 64;  // keys per LDS block
@@ -63,12 +63,6 @@ struct PrefillSmem {
 
 constexpr int kMaxPrefillSplits = 4;
 constexpr int kKsplit = 2;  // waves per query group (key slices of a block)
-
-// Split partials cross workgroups (and XCDs, each with its own L2) through
-// buffer loads and stores with the sc1 cache policy (device coherence), 16
-// bytes per lane so that every store fills whole 64-byte segments.
-constexpr int kSc1 = 16;                        // cache-policy bit of sc1
-constexpr int kBufferWord3 = 0x00020000;        // raw 32-bit buffer, no swizzle
 
 // V^T is stored d-major with the 4-key quads of each row permuted by
 // ((d >> 2) ^ (d >> 4)) & 15: with a 80-element pitch the staging writes
@@ -459,18 +453,13 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   const size_t tile = (size_t)h * nqt + qt;
   float* rec_tile = p.part + tile * p.nsplit * REC;
   const int slot = qg * 64 + lane;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      rec_tile, 0, (int)(ns * REC * sizeof(float)), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rsrc = coherent_rsrc(rec_tile, ns * REC * sizeof(float));
   if (owner) {
     const uint32_t rec = split * REC * sizeof(float);
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[t]), rsrc,
-                                             rec + (t * 256 + slot) * 16, 0, kSc1);
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m), rsrc,
-                                          rec + (DT * 4 * 256 + slot) * 4, 0, kSc1);
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lsum), rsrc,
-                                          rec + (DT * 4 * 256 + 256 + slot) * 4, 0, kSc1);
+    for (int t = 0; t < DT; ++t) st_coherent4(rsrc, rec + (t * 256 + slot) * 16, o[t]);
+    st_coherent(rsrc, rec + (DT * 4 * 256 + slot) * 4, m);
+    st_coherent(rsrc, rec + (DT * 4 * 256 + 256 + slot) * 4, lsum);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -495,11 +484,8 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
         ls[s2] = lsum;
       } else if (s2 < (int)ns) {
         const uint32_t rec = s2 * REC * sizeof(float);
-        ms[s2] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, rec + (DT * 4 * 256 + slot) * 4, 0, kSc1));
-        ls[s2] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, rec + (DT * 4 * 256 + 256 + slot) * 4,
-                                                        0, kSc1));
+        ms[s2] = ld_coherent(rsrc, rec + (DT * 4 * 256 + slot) * 4);
+        ls[s2] = ld_coherent(rsrc, rec + (DT * 4 * 256 + 256 + slot) * 4);
       }
     }
     float mm = ms[0];
@@ -522,8 +508,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
           const uint32_t rec = s2 * REC * sizeof(float);
 #pragma unroll
           for (int t = 0; t < DT; ++t)
-            os[t] = __builtin_bit_cast(
-                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, rec + (t * 256 + slot) * 16, 0, kSc1));
+            os[t] = ld_coherent4(rsrc, rec + (t * 256 + slot) * 16);
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) acc[t] += f * os[t];
