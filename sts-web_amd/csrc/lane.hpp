@@ -1,7 +1,8 @@
 // lane.hpp -- cross-lane exchanges inside a 64-wide CDNA wavefront.
 //
 // DPP row operations act within 16-lane rows; ds_swizzle bitmask mode acts
-// within 32-lane halves; a 32-lane exchange goes through ds_bpermute.
+// within 32-lane halves; a 32-lane exchange goes through ds_bpermute, or, for
+// reductions, through the gfx950 permlane swaps at the end of this file.
 // All exchanges here are involutions, so both partners see each other.
 #pragma once
 
@@ -38,6 +39,28 @@ __device__ __forceinline__ float xchg(float x) {
   else if constexpr (LEVEL == 2) return dpp_f32<kDppRowHalfMirror>(x);
   else if constexpr (LEVEL == 3) return dpp_f32<kDppRowMirror>(x);
   else return swizzle_xor16(x);
+}
+
+// gfx950 v_permlane16_swap / v_permlane32_swap called with x in both
+// operands return a pair that holds, on every lane, x itself and the value of
+// the partner lane (lane ^ 16, resp. lane ^ 32), in an order that depends on
+// the lane.  A commutative op of the pair is therefore x op partner(x) on
+// every lane, computed on the VALU without a trip through the LDS unit.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 }  // namespace sts

@@ -14,8 +14,8 @@
 // identically in V^T and P^T, so P never goes through LDS.  Each query's max
 // and sum are reduced over the 4 lanes {l%16 + 16g} that hold its keys.
 //
-//   BF16 = true : f32 K/V/Q rounded to bf16 while staging, v_mfma_f32_16x16x32_bf16
-//                 (16x16x16 for 16-key slices), f32 softmax and accumulation.
+//   BF16 = true : f32 K/V/Q rounded to bf16 while staging, v_mfma_f32_16x16x32_bf16,
+//                 f32 softmax and accumulation.
 //   BF16 = false: f32 throughout, v_mfma_f32_16x16x4f32.
 //
 // The f32 variant also splits each tile's key range over up to four
@@ -72,10 +72,10 @@ __device__ __forceinline__ int vt_col(int d, int quad) {
   return 4 * (quad ^ (((d >> 2) ^ (d >> 4)) & 15));
 }
 
-// KSPLIT waves share each group of 16 queries: wave w handles queries
-// 16 * (w % 4) .. +15 of the tile and the key slice w / 4 (64 / KSPLIT keys)
-// of every 64-key block, with its own online softmax; the slices merge once
-// at the end.  More waves per SIMD hide the latency of each wave's serial
+// KSPLIT (= 2) waves share each group of 16 queries: wave w handles queries
+// 16 * (w % 4) .. +15 of the tile and the key slice w / 4 (32 keys) of every
+// 64-key block, with its own online softmax; the slices merge once at the
+// end.  More waves per SIMD hide the latency of each wave's serial
 // softmax/MFMA chain.
 template <int D, bool BF16, int KSPLIT>
 __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillParams p) {
@@ -90,8 +90,12 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   constexpr int KPER = kBK * C4 / NT;  // K float4 per thread per block
   constexpr int VSQ = (kBK / 4) * C4;  // V 4-key x 4-dim squares per block
   constexpr int VPER = VSQ >= NT ? VSQ / NT : 1;
-  static_assert(KPER >= 1 && TW >= 1, "tile shape");
-  __shared__ Smem sm;
+  static_assert(KPER >= 1 && TW == 2, "tile shape: 32-key slices");
+  // bf16 tiles are double-buffered (block i+1 is staged while block i is
+  // computed, one barrier per block); f32 tiles are twice as large and use one
+  // buffer with a barrier on each side of the staging.
+  constexpr int NBUF = BF16 ? 2 : 1;
+  __shared__ Smem sm_buf[NBUF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -218,7 +222,8 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
               floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo[KPER + 4 * i + r4], so, 0));
     }
   };
-  auto stage = [&](const Buf& b) {
+  auto stage = [&](const Buf& b, int nb_) {
+    Smem& sm = sm_buf[nb_];
 #pragma unroll
     for (int i = 0; i < KPER; ++i) {
       const int key = tid / C4 + i * (NT / C4);
@@ -258,28 +263,55 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
 
   const uint32_t nblk = (kb_end - kb_begin + kBK - 1) / kBK;
   // One block out of LDS: S^T, online softmax, O^T update.
-  auto compute = [&](uint32_t kb) {
+  auto compute = [&](uint32_t kb, int nb_, bool active) {
+    const Smem& sm = sm_buf[nb_];
     const uint32_t k0 = kb + kslice * KW;  // first key of this wave's slice
-    if (k0 > w_wave) return;               // every key of the slice is masked for this wave
+    if (!active || k0 > w_wave) return;    // every key of the slice is masked for this wave
     const bool unmasked = k0 + KW <= kend && k0 + KW - 1 <= w_first;
 
-    // S^T tiles t: keys k0 + 16t + 4g + j, query qi.
+    // S^T tiles t: keys k0 + 16t + 4g + j, query qi.  The bf16 operands of
+    // the whole block (K for S^T, V^T for O^T) are read from LDS first, so
+    // the reads overlap each other, the MFMAs and the softmax.
+    const int q0 = kslice * (KW / 4);  // first 4-key quad of the slice
     floatx4 s[TW];
+    [[maybe_unused]] bf16x8 vop[DT];
+    if constexpr (BF16) {
+      bf16x8 kop[TW][QN];
 #pragma unroll
-    for (int t = 0; t < TW; ++t) {
-      const int krow = kslice * KW + 16 * t + l16;
-      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < TW; ++t)
 #pragma unroll
-      for (int a = 0; a < QN; ++a) {
-        if constexpr (BF16) {
-          const bf16x8 kop = *reinterpret_cast<const bf16x8*>(&sm.ks[krow * KP + a * 32 + g * 8]);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[a], s[t], 0, 0, 0);
-        } else {
-          const float4 kf = *reinterpret_cast<const float4*>(&sm.ks[krow * KP + a * 16 + g * 4]);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qop[a].x, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qop[a].y, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qop[a].z, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qop[a].w, s[t], 0, 0, 0);
+        for (int a = 0; a < QN; ++a)
+          kop[t][a] = *reinterpret_cast<const bf16x8*>(
+              &sm.ks[(kslice * KW + 16 * t + l16) * KP + a * 32 + g * 8]);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int d = 16 * t + l16;
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + g)]);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 4 + g)]);
+        vop[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int t = 0; t < TW; ++t) {
+        s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int a = 0; a < QN; ++a)
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[t][a], qop[a], s[t], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < TW; ++t) {
+        const int krow = kslice * KW + 16 * t + l16;
+        float4 kf[QN];
+#pragma unroll
+        for (int a = 0; a < QN; ++a)
+          kf[a] = *reinterpret_cast<const float4*>(&sm.ks[krow * KP + a * 16 + g * 4]);
+        s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int a = 0; a < QN; ++a) {
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].x, qop[a].x, s[t], 0, 0, 0);
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].y, qop[a].y, s[t], 0, 0, 0);
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].z, qop[a].z, s[t], 0, 0, 0);
+          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].w, qop[a].w, s[t], 0, 0, 0);
         }
       }
     }
@@ -303,8 +335,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
           mx = fmaxf(mx, x);
         }
     }
-    mx = fmaxf(mx, swizzle_xor16(mx));
-    mx = fmaxf(mx, xor32(mx));
+    mx = max_xor32(max_xor16(mx));
     const float mn = fmaxf(m, mx);
     const float alpha = fast_exp2(m - mn);
     m = mn;
@@ -317,8 +348,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
         s[t][j] = e;
         ps += e;
       }
-    ps += swizzle_xor16(ps);
-    ps += xor32(ps);
+    ps = sum_xor32(sum_xor16(ps));
     lsum = lsum * alpha + ps;
     // Rescale only when some lane's running max moved (alpha == 1 otherwise).
     if (__any(alpha != 1.f)) {
@@ -326,46 +356,17 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
       for (int t = 0; t < DT; ++t) o[t] *= alpha;
     }
 
-    // O^T += V^T P^T over this wave's KW keys.
-    const int q0 = kslice * (KW / 4);  // first 4-key quad of the slice
+    // O^T += V^T P^T over this wave's 32 keys.
     if constexpr (BF16) {
-      if constexpr (KW >= 32) {
+      bf16x8 pb;
 #pragma unroll
-        for (int kk = 0; kk < KW / 32; ++kk) {
-          bf16x8 pb;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            pb[j] = (__bf16)s[2 * kk][j];
-            pb[4 + j] = (__bf16)s[2 * kk + 1][j];
-          }
-#pragma unroll
-          for (int t = 0; t < DT; ++t) {
-            const int d = 16 * t + l16;
-            const bf16x4 lo =
-                *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 8 * kk + g)]);
-            const bf16x4 hi =
-                *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 8 * kk + 4 + g)]);
-            bf16x8 vop;
-            vop[0] = lo[0]; vop[1] = lo[1]; vop[2] = lo[2]; vop[3] = lo[3];
-            vop[4] = hi[0]; vop[5] = hi[1]; vop[6] = hi[2]; vop[7] = hi[3];
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pb, o[t], 0, 0, 0);
-          }
-        }
-      } else {
-        // 16 keys: the S^T tile's lane layout (keys 4g..4g+3) is the B operand
-        // of the 16x16x16 product directly.
-        bf16x4 pb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pb[j] = (__bf16)s[0][j];
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const int d = 16 * t + l16;
-          const bf16x4 vop = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + g)]);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vop),
-                                                          __builtin_bit_cast(s16x4, pb), o[t], 0,
-                                                          0, 0);
-        }
+      for (int j = 0; j < 4; ++j) {
+        pb[j] = (__bf16)s[0][j];
+        pb[4 + j] = (__bf16)s[1][j];
       }
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[t], pb, o[t], 0, 0, 0);
     } else {
 #pragma unroll
       for (int t = 0; t < DT; ++t)
@@ -383,20 +384,38 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   };
 
   // One block in flight in registers while the previous one computes.
-  fetch(buf, kb_begin, true);
-  for (uint32_t i = 0; i < nblk; ++i) {
-    const uint32_t kb = kb_begin + i * kBK;
-    __syncthreads();  // the previous block's LDS reads are done
-    stage(buf);
+  auto blk = [&](uint32_t i) { return kb_begin + min(i, nblk - 1) * kBK; };
+  if constexpr (NBUF == 2) {
+    // While block i is computed from one LDS buffer, block i+1 (in registers
+    // since the previous trip) is staged into the other and block i+2 is
+    // fetched.  The other buffer was last read by block i-1, which every wave
+    // finished before the previous barrier.
+    fetch(buf, blk(0), true);
+    stage(buf, 0);
+    fetch(buf, blk(1), nblk > 1);
     __syncthreads();
-    fetch(buf, min(kb + kBK, kb_begin + (nblk - 1) * kBK), i + 1 < nblk);
-    compute(kb);
+    for (uint32_t i = 0; i < nblk; ++i) {
+      compute(blk(i), i & 1, true);
+      if (i + 1 < nblk) stage(buf, (i + 1) & 1);
+      fetch(buf, blk(i + 2), i + 2 < nblk);
+      __syncthreads();
+    }
+  } else {
+    fetch(buf, kb_begin, true);
+    for (uint32_t i = 0; i < nblk; ++i) {
+      const uint32_t kb = kb_begin + i * kBK;
+      __syncthreads();  // the previous block's LDS reads are done
+      stage(buf, 0);
+      __syncthreads();
+      fetch(buf, blk(i + 1), i + 1 < nblk);
+      compute(kb, 0, true);
+    }
   }
 
   // Merge the key slices of each query group: slice r > 0 parks (m, l, O^T)
   // in LDS (reusing the K/V tiles), slice 0 folds it in; one round per slice.
   if constexpr (KSPLIT > 1) {
-    float* red = reinterpret_cast<float*>(&sm);  // [4 groups][64 lanes][DT*4 + 2]
+    float* red = reinterpret_cast<float*>(&sm_buf[0]);  // [4 groups][64 lanes][DT*4 + 2]
     constexpr int RS = DT * 4 + 2;
     static_assert(4 * 64 * RS * sizeof(float) <= sizeof(Smem), "merge scratch");
 #pragma unroll
