@@ -7,8 +7,9 @@ seeded offset so reads wrap.  Every layer has its own 98 MB cache (2.36 GB,
 beyond the 256 MB MALL).  Inputs are resident in HBM before timing.
 
 Also reported (extra fields): decode without the append (sts_kv_attend),
-chunked prefill (config 3, f32 and bf16-MFMA), depformer frame (config 4) and
-ragged multi-stream decode (config 5); and the CPU baseline -- the oracle's
+chunked prefill (config 3, f32 and bf16-MFMA), depformer frame (config 4),
+ragged multi-stream decode (config 5), the Q4_K projections around attention
+(in_proj / out_proj per frame, FFN shapes); and the CPU baseline -- the oracle's
 restatement of the reference shader, timed on this host's cores on a bounded
 sample of the same workload.
 
@@ -229,6 +230,74 @@ def bench_ragged(torch, sts, stream, steps, warmup):
             "mean_len": total_rows / (LAYERS * B)}
 
 
+def q4k_random(torch, g, n, k):
+    """Random Q4_K blocks on the device: quant and scale bytes uniform, d and
+    dmin finite positive halves in [2^-14, 2^-4)."""
+    nb = n * k // 256
+    raw = torch.randint(0, 256, (nb, 144), generator=g, device="cuda", dtype=torch.uint8)
+    half = torch.randint(0x0400, 0x2C00, (nb, 2), generator=g, device="cuda", dtype=torch.int32)
+    for i in range(2):
+        raw[:, 2 * i] = (half[:, i] & 0xFF).to(torch.uint8)
+        raw[:, 2 * i + 1] = (half[:, i] >> 8).to(torch.uint8)
+    return raw.reshape(-1)
+
+
+def bench_q4k(torch, sts, stream, steps, warmup):
+    """The Q4_K projections on either side of attention, batch 1: per temporal
+    frame 24 layers x (in_proj [12288, 4096] + out_proj [4096, 4096] with the
+    residual), each layer with its own weights (905 MB, beyond the MALL),
+    launched eagerly and replayed from a HIP graph; plus single-launch rates of
+    the FFN shapes linear_in [22528, 4096] and linear_out [4096, 11264]."""
+    g = torch.Generator(device="cuda").manual_seed(6)
+    K = 4096
+    layers = [(sts.Q4KTensor(q4k_random(torch, g, 3 * K, K), (3 * K, K)),
+               sts.Q4KTensor(q4k_random(torch, g, K, K), (K, K))) for _ in range(LAYERS)]
+    x = torch.randn((1, 1, K), generator=g, device="cuda")
+    qkv = torch.empty((1, 1, 3 * K), device="cuda")
+    y = torch.empty((1, 1, K), device="cuda")
+
+    def frame():
+        for wi, wo in layers:
+            sts.q4k_matmul(x, wi, out=qkv, stream=stream)
+            sts.q4k_matmul(x, wo, residual=x, out=y, stream=stream)
+
+    for _ in range(warmup):
+        frame()
+    with Timer(torch, stream) as te:
+        for _ in range(steps):
+            frame()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        frame()
+    for _ in range(warmup):
+        graph.replay()
+    with Timer(torch, stream) as tg:
+        for _ in range(steps):
+            graph.replay()
+    w_bytes = LAYERS * 4 * K * K // 256 * 144
+    io_bytes = LAYERS * 4 * (K + 3 * K + K + K + K)  # x twice, qkv, residual, y
+    us = tg.ms * 1e3 / steps
+    res = {"us_per_frame": us, "eager_us_per_frame": te.ms * 1e3 / steps,
+           "weight_bytes_per_frame": w_bytes,
+           "gbs": (w_bytes + io_bytes) / (us * 1e-6) / 1e9}
+    res["frac"] = res["gbs"] / HBM_PEAK_GBS
+    for name, (n, k) in (("linear_in", (22528, K)), ("linear_out", (K, 11264))):
+        ws = [sts.Q4KTensor(q4k_random(torch, g, n, k), (n, k)) for _ in range(4)]
+        xi = torch.randn((1, 1, k), generator=g, device="cuda")
+        yo = torch.empty((1, 1, n), device="cuda")
+        for w in ws:
+            sts.q4k_matmul(xi, w, out=yo, stream=stream)
+        with Timer(torch, stream) as t:
+            for _ in range(steps):
+                for w in ws:
+                    sts.q4k_matmul(xi, w, out=yo, stream=stream)
+        us_l = t.ms * 1e3 / (steps * len(ws))
+        res[name + "_us_per_launch"] = us_l
+        res[name + "_gbs"] = n * k // 256 * 144 / (us_l * 1e-6) / 1e9
+        del ws
+    return res
+
+
 def cpu_baseline(torch, dec):
     """The oracle's restatement of shader_attention.wgsl, on this host's cores,
     over 2 of the 24 layers of the decode workload, scaled to us/frame."""
@@ -305,6 +374,9 @@ def main():
             log("bench: ragged (config 5)")
             extra["ragged"] = bench_ragged(torch, sts, stream, max(2, args.steps // 4),
                                            min(args.warmup, 2))
+        if want("q4k"):
+            log("bench: q4k projections")
+            extra["q4k"] = bench_q4k(torch, sts, stream, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
@@ -352,6 +424,9 @@ def main():
         r = extra["ragged"]
         line["ragged"] = {k: round(v, 2) for k, v in r.items()}
         line["ragged"]["frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    if "q4k" in extra:
+        line["q4k_projections"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                   for k, v in extra["q4k"].items()}
     if cpu is not None:
         line["gpu_vs_cpu"] = round(cpu["value"] / dec["us_per_frame"], 1)
     print(json.dumps(line), flush=True)

@@ -266,6 +266,29 @@ int sts_kv_prefill(sts_kv_cache* cache, const float* q, const float* k_new,
                    const float* v_new, float* out, uint64_t seq, float scale,
                    int precision, void* stream);
 
+/* ---- Q4_K projections (the matvecs on either side of attention) --------- */
+
+/*
+ * y = W x (+ residual) for a Q4_K weight matrix W [n][k]: q4k_matmul with
+ * M = 1 and q4k_matmul_with_residual (gguf.rs:808-905, kernel
+ * wgsl/shader_q4k_matvec.wgsl) -- the in_proj / out_proj (and FFN) products
+ * of every decode step (model.rs:730, :834).  `weights` holds the tensor as
+ * the GGUF file stores it (Q4KTensor::from_q4k_bytes, gguf.rs:530-563):
+ * n rows of k/256 super-blocks of 144 bytes.  x is [batch][k] (the
+ * reference's [B, 1, K] input), y [batch][n], residual [batch][n] or NULL.
+ * k must be a multiple of 256 and at most 16384; weights and x 16-byte
+ * aligned.  Each batch row reads the whole weight matrix once.
+ */
+int sts_q4k_matvec(const uint8_t* weights, const float* x, const float* residual, float* y,
+                   uint32_t batch, uint32_t k, uint32_t n, void* stream);
+
+/*
+ * Dequantise a Q4_K matrix to f32 out [n][k], each weight rounded as the
+ * reference shader computes it: d1 = d*scale, m1 = dmin*min, w = q*d1 - m1
+ * (shader_q4k_matvec.wgsl:117-136).
+ */
+int sts_q4k_dequant(const uint8_t* weights, float* out, uint32_t k, uint32_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

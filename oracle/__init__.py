@@ -56,6 +56,14 @@ def _load():
                                    _u32, _u32, ctypes.c_double]),
         "orc_prefill_seq_wgsl": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, _u32,
                                         _u32, _u32, ctypes.c_float]),
+        "orc_f16_to_f32_n": (None, [ctypes.c_void_p, _f32p, _u64]),
+        "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+        "orc_q4k_scale_min": (None, [ctypes.c_void_p, _u32, ctypes.POINTER(_u32),
+                                     ctypes.POINTER(_u32)]),
+        "orc_q4k_dequant": (None, [ctypes.c_void_p, _u32, _u32, _f32p]),
+        "orc_q4k_quantize": (None, [_f32p, _u32, _u32, ctypes.c_void_p]),
+        "orc_q4k_matvec_wgsl": (None, [ctypes.c_void_p, _f32p, _f32p, _u32, _u32, _u32]),
+        "orc_q4k_matvec_f64": (None, [ctypes.c_void_p, _f32p, _f64p, _u32, _u32, _u32]),
         "orc_num_threads": (ctypes.c_int, []),
         "orc_set_num_threads": (None, [ctypes.c_int]),
     }
@@ -236,3 +244,85 @@ def num_threads() -> int:
 
 def set_num_threads(n: int) -> None:
     lib().orc_set_num_threads(n)
+
+
+# ---- Q4_K -------------------------------------------------------------------
+
+Q4K_BLOCK_BYTES = 144
+QK_K = 256
+
+
+def _u8(a):
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def f16_to_f32(bits):
+    """unpack2x16float (shader_q4k_matvec.wgsl:82) elementwise on a uint16 array."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().orc_f16_to_f32_n(b.ctypes.data_as(ctypes.c_void_p), _p32(out), b.size)
+    return out
+
+
+def f32_to_f16(x):
+    """Round-to-nearest-even f32 -> f16 bits (scalar)."""
+    return int(lib().orc_f32_to_f16(float(np.float32(x))))
+
+
+def q4k_scale_min(scales12, j):
+    s, _ = _u8(scales12)
+    sc, mn = _u32(), _u32()
+    lib().orc_q4k_scale_min(s.ctypes.data_as(ctypes.c_void_p), j, ctypes.byref(sc),
+                            ctypes.byref(mn))
+    return sc.value, mn.value
+
+
+def q4k_dequant(blocks, N, K):
+    """[N][K] f32 weights from N*K/256 blocks of 144 bytes."""
+    b, bp = _u8(blocks)
+    assert b.size == N * K // QK_K * Q4K_BLOCK_BYTES
+    w = np.empty((N, K), np.float32)
+    lib().orc_q4k_dequant(bp, N, K, _p32(w))
+    return w
+
+
+def q4k_quantize(x):
+    """scripts/quantize.py quantize_q4_k applied row by row to x [N][K]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N, K = x.shape
+    out = np.empty(N * K // QK_K * Q4K_BLOCK_BYTES, np.uint8)
+    lib().orc_q4k_quantize(_p32(x), N, K, out.ctypes.data_as(ctypes.c_void_p))
+    return out
+
+
+def q4k_matvec_wgsl(blocks, x, N):
+    """x [B][K] -> y [B][N] in the matvec shader's f32 order."""
+    b, bp = _u8(blocks)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, K = x.shape
+    y = np.empty((B, N), np.float32)
+    lib().orc_q4k_matvec_wgsl(bp, _p32(x), _p32(y), B, K, N)
+    return y
+
+
+def q4k_matvec_f64(blocks, x, N):
+    b, bp = _u8(blocks)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, K = x.shape
+    y = np.empty((B, N), np.float64)
+    lib().orc_q4k_matvec_f64(bp, _p32(x), y.ctypes.data_as(_f64p), B, K, N)
+    return y
+
+
+def q4k_random_blocks(seed, N, K):
+    """Random Q4_K blocks: every scale/quant byte uniform, d and dmin finite
+    positive halves in [2^-14, 2^-4) so weights stay O(1)."""
+    rng = np.random.default_rng(seed)
+    nb = N * K // QK_K
+    blk = rng.integers(0, 256, size=(nb, Q4K_BLOCK_BYTES), dtype=np.uint8)
+    for off in (0, 2):
+        half = rng.integers(0x0400, 0x2C00, size=nb, dtype=np.uint16)  # exponents 1..10
+        blk[:, off] = (half & 0xFF).astype(np.uint8)
+        blk[:, off + 1] = (half >> 8).astype(np.uint8)
+    return blk.reshape(-1)

@@ -353,6 +353,219 @@ void orc_prefill_seq_wgsl(const float* q, const float* kc, const float* vc, floa
   free(vg);
 }
 
+/* ------------------------------------------------------------------------ */
+/* Q4_K                                                                       */
+/* ------------------------------------------------------------------------ */
+
+enum { QK_K = 256, Q4K_BYTES = 144 };
+
+/* WGSL unpack2x16float, which every Q4_K shader uses for d and dmin
+ * (shader_q4k_matvec.wgsl:82): exact IEEE binary16 -> binary32.  Subnormals
+ * are m * 2^-24 exactly; exponent 31 gives inf or NaN.  (The CPU helper
+ * gguf.rs:65-88 f16_to_f32 returns half the value for subnormals; it is not
+ * on the matvec path.) */
+float orc_f16_to_f32(uint16_t bits) {
+  const uint32_t sign = (uint32_t)(bits >> 15) << 31;
+  const uint32_t exponent = (bits >> 10) & 0x1Fu;
+  const uint32_t mantissa = bits & 0x3FFu;
+  uint32_t out;
+  if (exponent == 0) {
+    float f = ldexpf((float)mantissa, -24);
+    memcpy(&out, &f, 4);
+    out |= sign;
+  } else if (exponent == 31) {
+    out = sign | (0xFFu << 23) | (mantissa << 13);
+  } else {
+    out = sign | ((exponent - 15u + 127u) << 23) | (mantissa << 13);
+  }
+  float f;
+  memcpy(&f, &out, 4);
+  return f;
+}
+
+void orc_f16_to_f32_n(const uint16_t* bits, float* out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(bits[i]);
+}
+
+/* Round-to-nearest-even f32 -> f16 (what numpy's astype(np.float16) does). */
+uint16_t orc_f32_to_f16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t absu = u & 0x7FFFFFFFu;
+  if (absu >= 0x7F800000u) /* inf or NaN */
+    return (uint16_t)(sign | 0x7C00u | (absu > 0x7F800000u ? 0x200u : 0u));
+  if (absu >= 0x477FF000u) /* rounds to >= 65520: overflow to inf */
+    return (uint16_t)(sign | 0x7C00u);
+  if (absu < 0x38800000u) { /* below 2^-14: f16 subnormal or zero */
+    if (absu < 0x33000000u) return (uint16_t)sign; /* below 2^-25: rounds to 0 */
+    const uint32_t e = absu >> 23;                 /* biased f32 exponent 102..112 */
+    const uint32_t mant = (absu & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 126u - e;               /* 14..24 */
+    uint32_t h = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((absu >> 13) - (112u << 10)); /* rebias exponent, keep 10 mantissa bits */
+  const uint32_t rem = absu & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+  return (uint16_t)(sign | h);
+}
+
+/* shader_q4k_matvec.wgsl:85-113. */
+void orc_q4k_scale_min(const uint8_t* q, uint32_t j, uint32_t* sc, uint32_t* mn) {
+  if (j < 4) {
+    *sc = q[j] & 63u;
+    *mn = q[j + 4] & 63u;
+  } else {
+    *sc = (q[j + 4] & 0xFu) | ((uint32_t)(q[j - 4] >> 6) << 4);
+    *mn = (uint32_t)(q[j + 4] >> 4) | ((uint32_t)(q[j] >> 6) << 4);
+  }
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* shader_q4k_matvec.wgsl:117-136: per iteration `it`, sub-blocks 2it (low
+ * nibbles) and 2it+1 (high nibbles) of qs bytes it*32 .. it*32+31. */
+void orc_q4k_dequant(const uint8_t* blocks, uint32_t N, uint32_t K, float* w) {
+  const uint32_t nb = K / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < (int64_t)N; ++n) {
+    for (uint32_t blk = 0; blk < nb; ++blk) {
+      const uint8_t* b = blocks + ((size_t)n * nb + blk) * Q4K_BYTES;
+      const float d = orc_f16_to_f32(rd16(b));
+      const float dmin = orc_f16_to_f32(rd16(b + 2));
+      float* out = w + (size_t)n * K + (size_t)blk * QK_K;
+      for (uint32_t it = 0; it < 4; ++it) {
+        uint32_t s0, m0, s1, m1;
+        orc_q4k_scale_min(b + 4, 2 * it, &s0, &m0);
+        orc_q4k_scale_min(b + 4, 2 * it + 1, &s1, &m1);
+        const float d1 = d * (float)s0, mm1 = dmin * (float)m0;
+        const float d2 = d * (float)s1, mm2 = dmin * (float)m1;
+        for (uint32_t j = 0; j < 32; ++j) {
+          const uint8_t byte = b[16 + it * 32 + j];
+          out[it * 64 + j] = (float)(byte & 0xF) * d1 - mm1;
+          out[it * 64 + 32 + j] = (float)(byte >> 4) * d2 - mm2;
+        }
+      }
+    }
+  }
+}
+
+/* scripts/quantize.py:162-253: per 32-weight sub-block, scale = (max-min)/15
+ * and min value = -min; d = max scale / 63, dmin = max min value / 63 (1.0
+ * when zero), both rounded to f16; 6-bit sub-block scales/mins and 4-bit
+ * quants by round-half-even (np.round) and clipping, all in f32. */
+void orc_q4k_quantize(const float* x, uint32_t N, uint32_t K, uint8_t* blocks) {
+  const uint32_t nb = K / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < (int64_t)N * nb; ++r) {
+    const float* v = x + (size_t)r * QK_K;
+    uint8_t* o = blocks + (size_t)r * Q4K_BYTES;
+    float raw_scale[8], raw_min[8], max_scale = 0.f, max_min = 0.f;
+    for (int j = 0; j < 8; ++j) {
+      float mn = v[j * 32], mx = v[j * 32];
+      for (int i = 1; i < 32; ++i) {
+        mn = fminf(mn, v[j * 32 + i]);
+        mx = fmaxf(mx, v[j * 32 + i]);
+      }
+      raw_scale[j] = mx > mn ? (mx - mn) / 15.0f : 0.f;
+      raw_min[j] = -mn;
+      if (j == 0 || raw_scale[j] > max_scale) max_scale = raw_scale[j];
+      if (j == 0 || raw_min[j] > max_min) max_min = raw_min[j];
+    }
+    const uint16_t d16 = orc_f32_to_f16(max_scale > 0.f ? max_scale / 63.0f : 1.0f);
+    const uint16_t dm16 = orc_f32_to_f16(max_min > 0.f ? max_min / 63.0f : 1.0f);
+    const float d = orc_f16_to_f32(d16), dmin = orc_f16_to_f32(dm16);
+    uint8_t sc[8], m[8];
+    for (int j = 0; j < 8; ++j) {
+      float a = d > 0.f ? nearbyintf(raw_scale[j] / d) : 0.f;
+      float b = dmin > 0.f ? nearbyintf(raw_min[j] / dmin) : 0.f;
+      a = a < 0.f ? 0.f : (a > 63.f ? 63.f : a);
+      b = b < 0.f ? 0.f : (b > 63.f ? 63.f : b);
+      sc[j] = (uint8_t)a;
+      m[j] = (uint8_t)b;
+    }
+    o[0] = (uint8_t)(d16 & 0xFF);
+    o[1] = (uint8_t)(d16 >> 8);
+    o[2] = (uint8_t)(dm16 & 0xFF);
+    o[3] = (uint8_t)(dm16 >> 8);
+    uint8_t* sb = o + 4;
+    for (int j = 0; j < 4; ++j) {
+      sb[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      sb[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+      sb[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+    uint8_t q[8][32];
+    for (int j = 0; j < 8; ++j) {
+      const float es = d * (float)sc[j], em = dmin * (float)m[j];
+      for (int i = 0; i < 32; ++i) {
+        float t = es > 0.f ? nearbyintf((v[j * 32 + i] + em) / es) : 0.f;
+        t = t < 0.f ? 0.f : (t > 15.f ? 15.f : t);
+        q[j][i] = (uint8_t)t;
+      }
+    }
+    for (int it = 0; it < 4; ++it)
+      for (int i = 0; i < 32; ++i)
+        o[16 + it * 32 + i] = (uint8_t)((q[2 * it][i] & 0xF) | ((q[2 * it + 1][i] & 0xF) << 4));
+  }
+}
+
+static inline float dot4(float a0, float a1, float a2, float a3, const float* b) {
+  return a0 * b[0] + a1 * b[1] + a2 * b[2] + a3 * b[3];
+}
+
+/* shader_q4k_matvec.wgsl:48-356 (the structure is the same for the chunked
+ * shared-memory input: chunks only move where x is read from). */
+void orc_q4k_matvec_wgsl(const uint8_t* blocks, const float* x, float* y, uint32_t B,
+                         uint32_t K, uint32_t N) {
+  const uint32_t nb = K / QK_K;
+#pragma omp parallel for schedule(static)
+  for (int64_t bn = 0; bn < (int64_t)B * N; ++bn) {
+    const uint32_t b = (uint32_t)(bn / N), n = (uint32_t)(bn % N);
+    const float* xb = x + (size_t)b * K;
+    float acc = 0.f;
+    for (uint32_t blk = 0; blk < nb; ++blk) {
+      const uint8_t* p = blocks + ((size_t)n * nb + blk) * Q4K_BYTES;
+      const float d = orc_f16_to_f32(rd16(p));
+      const float dmin = orc_f16_to_f32(rd16(p + 2));
+      for (uint32_t it = 0; it < 4; ++it) {
+        uint32_t s0, m0, s1, m1;
+        orc_q4k_scale_min(p + 4, 2 * it, &s0, &m0);
+        orc_q4k_scale_min(p + 4, 2 * it + 1, &s1, &m1);
+        const float d1 = d * (float)s0, mm1 = dmin * (float)m0;
+        const float d2 = d * (float)s1, mm2 = dmin * (float)m1;
+        const float* xlo = xb + blk * QK_K + it * 64;
+        const float* xhi = xlo + 32;
+        for (uint32_t w = 0; w < 8; ++w) {
+          const uint8_t* q = p + 16 + it * 32 + w * 4;
+          acc += dot4((float)(q[0] & 0xF) * d1 - mm1, (float)(q[1] & 0xF) * d1 - mm1,
+                      (float)(q[2] & 0xF) * d1 - mm1, (float)(q[3] & 0xF) * d1 - mm1, xlo + w * 4);
+          acc += dot4((float)(q[0] >> 4) * d2 - mm2, (float)(q[1] >> 4) * d2 - mm2,
+                      (float)(q[2] >> 4) * d2 - mm2, (float)(q[3] >> 4) * d2 - mm2, xhi + w * 4);
+        }
+      }
+    }
+    y[(size_t)b * N + n] = acc;
+  }
+}
+
+void orc_q4k_matvec_f64(const uint8_t* blocks, const float* x, double* y, uint32_t B,
+                        uint32_t K, uint32_t N) {
+  float* w = (float*)malloc(sizeof(float) * (size_t)N * K);
+  orc_q4k_dequant(blocks, N, K, w);
+#pragma omp parallel for schedule(static)
+  for (int64_t bn = 0; bn < (int64_t)B * N; ++bn) {
+    const uint32_t b = (uint32_t)(bn / N), n = (uint32_t)(bn % N);
+    double acc = 0.0;
+    for (uint32_t k = 0; k < K; ++k) acc += (double)w[(size_t)n * K + k] * (double)x[(size_t)b * K + k];
+    y[bn] = acc;
+  }
+  free(w);
+}
+
 int orc_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -113,6 +113,45 @@ void orc_prefill_seq_wgsl(const float* q, const float* kc, const float* vc, floa
                           uint32_t S, uint32_t H, uint32_t D, uint32_t M, uint32_t start,
                           uint32_t len, float scale);
 
+/* ---- Q4_K weights and matvec (gguf.rs, wgsl/shader_q4k_matvec.wgsl) ------
+ * A Q4_K matrix [N][K] is N rows of K/256 super-blocks of 144 bytes:
+ * d (f16), dmin (f16), 12 bytes of packed 6-bit sub-block scales and mins,
+ * 128 bytes of 4-bit quants (shader_q4k_matvec.wgsl:13-19).  Weight k of
+ * sub-block j is (d*scale_j)*q - (dmin*min_j). */
+
+/* WGSL unpack2x16float as the Q4_K shaders use it (shader_q4k_matvec.wgsl:82):
+ * exact binary16 -> binary32. */
+float orc_f16_to_f32(uint16_t bits);
+
+/* orc_f16_to_f32 over n values (elementwise; for tests). */
+void orc_f16_to_f32_n(const uint16_t* bits, float* out, uint64_t n);
+
+/* f32 -> f16 bits, round to nearest even (numpy's astype(float16), which
+ * scripts/quantize.py:193-194 uses). */
+uint16_t orc_f32_to_f16(float x);
+
+/* shader_q4k_matvec.wgsl:85-113 (= shader_q4k.wgsl:48-63): 6-bit scale and
+ * min of sub-block j (0..7) from the 12 packed bytes. */
+void orc_q4k_scale_min(const uint8_t* scales12, uint32_t j, uint32_t* sc, uint32_t* mn);
+
+/* Dequantised weights w[N][K], in the shader's f32 order
+ * (shader_q4k_matvec.wgsl:117-136): d1 = d*scale, m1 = dmin*min, w = q*d1 - m1. */
+void orc_q4k_dequant(const uint8_t* blocks, uint32_t N, uint32_t K, float* w);
+
+/* scripts/quantize.py:162-253 quantize_q4_k, row by row (K % 256 == 0). */
+void orc_q4k_quantize(const float* x, uint32_t N, uint32_t K, uint8_t* blocks);
+
+/* shader_q4k_matvec.wgsl:48-356 for each output y[b][n] (x [B][K], y [B][N]):
+ * acc over super-blocks in order; per block 4 iterations of 8 words; per
+ * word acc += dot(lo) then acc += dot(hi), dot evaluated left to right
+ * (WGSL leaves the order of dot() to the implementation). */
+void orc_q4k_matvec_wgsl(const uint8_t* blocks, const float* x, float* y, uint32_t B,
+                         uint32_t K, uint32_t N);
+
+/* y = W x in double over the dequantised weights. */
+void orc_q4k_matvec_f64(const uint8_t* blocks, const float* x, double* y, uint32_t B,
+                        uint32_t K, uint32_t N);
+
 /* Number of OpenMP threads the oracle uses (for the CPU-baseline record). */
 int orc_num_threads(void);
 void orc_set_num_threads(int n);

@@ -14,6 +14,7 @@
 #include "common.hpp"
 #include "decode.hpp"
 #include "prefill.hpp"
+#include "q4k.hpp"
 
 using sts::fail;
 
@@ -531,3 +532,35 @@ int sts_kv_prefill(sts_kv_cache* cache, const float* q, const float* k_new, cons
 }
 
 }  // extern "C"
+
+// ---- Q4_K ------------------------------------------------------------------
+
+extern "C" int sts_q4k_matvec(const uint8_t* weights, const float* x, const float* residual,
+                              float* y, uint32_t batch, uint32_t k, uint32_t n, void* stream) {
+  sts::clear_error();
+  STS_CHECK(weights && x && y, "null pointer argument");
+  STS_CHECK(batch >= 1 && batch <= 65535, "batch %u out of range 1..65535", batch);
+  STS_CHECK(n >= 1, "empty shape");
+  STS_CHECK(k >= 256 && k % 256 == 0 && k <= 16384,
+            "k = %u must be a multiple of 256 in 256..16384", k);
+  STS_CHECK(aligned16(weights) && aligned16(x), "weights and x must be 16-byte aligned");
+  sts::Q4kParams p;
+  p.w = weights;
+  p.x = x;
+  p.res = residual;
+  p.y = y;
+  p.B = batch;
+  p.K = k;
+  p.N = n;
+  return sts::launch_q4k_matvec(p, as_stream(stream));
+}
+
+extern "C" int sts_q4k_dequant(const uint8_t* weights, float* out, uint32_t k, uint32_t n,
+                               void* stream) {
+  sts::clear_error();
+  STS_CHECK(weights && out, "null pointer argument");
+  STS_CHECK(n >= 1, "empty shape");
+  STS_CHECK(k >= 256 && k % 256 == 0, "k = %u must be a positive multiple of 256", k);
+  STS_CHECK(aligned16(weights) && aligned16(out), "weights and out must be 16-byte aligned");
+  return sts::launch_q4k_dequant(weights, out, n, k, as_stream(stream));
+}

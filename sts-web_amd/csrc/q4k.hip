@@ -1,0 +1,286 @@
+// q4k.hip -- Q4_K dequantisation and matrix-vector product for gfx950.
+//
+// Reference: crates/sts-wasm/src/gguf.rs:808-905 (q4k_matmul with M = 1, the
+// single-token path, and q4k_matmul_with_residual), whose kernel is
+// wgsl/shader_q4k_matvec.wgsl: one output per thread, dequantising
+// w = (d*scale)*q - (dmin*min) weight by weight in f32.
+//
+// Work split.  A row of K weights is S = K/64 slots of 64 consecutive
+// weights: slot s is iteration it = s%4 of super-block s/4, i.e. 32 quant
+// bytes whose low nibbles are sub-block 2it and high nibbles sub-block 2it+1
+// (weights 64s .. 64s+63), plus the block's 16-byte header (d, dmin, packed
+// scales).  Lane l of a wave owns slot 64*kp + l, where kp numbers the KP
+// waves that share a row when K > 4096; it keeps the 64 x values of its slot
+// in registers for the whole launch and walks rows, adding per row
+//     d1 * sum(q_lo * x_lo) - m1 * sum(x_lo) + d2 * sum(q_hi * x_hi) - m2 * sum(x_hi)
+// with the two sums of x computed once.  Per row a lane loads 48 bytes; the
+// lanes of a wave together read the row as one contiguous stream (2304
+// bytes at K = 4096).  Rows are dealt round-robin to the row groups of the
+// grid, U rows per group in flight at a time.  The regrouping changes the
+// rounding of the sum (tolerance-checked against the shader-order oracle),
+// not the weights: the dequantisation kernel below reproduces the shader's
+// f32 weights bit for bit.
+//
+// HBM-bound: 0.5625 bytes and 2 flops per weight (x and y are negligible).
+#include <algorithm>
+#include <cstdint>
+
+#include "common.hpp"
+#include "lane.hpp"
+#include "q4k.hpp"
+
+namespace sts {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Exact binary16 -> binary32 (v_cvt_f32_f16), as WGSL unpack2x16float.
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xFFFFu));
+}
+
+// 6-bit scale and min of sub-block j from the packed scale bytes held in
+// s0 (bytes 0-3), s1 (4-7), s2 (8-11); shader_q4k_matvec.wgsl:85-113.
+__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j,
+                                          uint32_t& sc, uint32_t& mn) {
+  const uint32_t sh = 8u * (j & 3u);
+  const uint32_t b0 = (s0 >> sh) & 0xFFu, b1 = (s1 >> sh) & 0xFFu, b2 = (s2 >> sh) & 0xFFu;
+  if (j < 4) {
+    sc = b0 & 63u;
+    mn = b1 & 63u;
+  } else {
+    sc = (b2 & 0xFu) | ((b0 >> 6) << 4);
+    mn = (b2 >> 4) | ((b1 >> 6) << 4);
+  }
+}
+
+// d1*sum(q_lo*x_lo) - m1*sum(x_lo) + d2*sum(q_hi*x_hi) - m2*sum(x_hi) for one slot.
+__device__ __forceinline__ float slot_dot(u32x4 hd, u32x4 qa, u32x4 qb, uint32_t jl,
+                                          const float (&xv)[64], float sxl, float sxh) {
+  const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+  uint32_t scl, mnl, sch, mnh;
+  scale_min(hd.y, hd.z, hd.w, jl, scl, mnl);
+  scale_min(hd.y, hd.z, hd.w, jl + 1, sch, mnh);
+  const uint32_t words[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  // Four independent chains per half, so consecutive FMAs do not wait on
+  // each other.
+  float ql[4] = {0.f, 0.f, 0.f, 0.f}, qh[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t lo = words[w] & 0x0F0F0F0Fu;
+    uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;
+    // Opaque to the optimiser, so that each byte below becomes one
+    // v_cvt_f32_ubyte{0..3} instead of a bit-field extract plus a convert.
+    asm("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ql[i] = fmaf((float)((lo >> (8 * i)) & 0xFFu), xv[4 * w + i], ql[i]);
+      qh[i] = fmaf((float)((hi >> (8 * i)) & 0xFFu), xv[32 + 4 * w + i], qh[i]);
+    }
+  }
+  const float qls = (ql[0] + ql[1]) + (ql[2] + ql[3]);
+  const float qhs = (qh[0] + qh[1]) + (qh[2] + qh[3]);
+  const float d1 = d * (float)scl, m1 = dmin * (float)mnl;
+  const float d2 = d * (float)sch, m2 = dmin * (float)mnh;
+  return (d1 * qls - m1 * sxl) + (d2 * qhs - m2 * sxh);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x += xchg<0>(x);
+  x += xchg<1>(x);
+  x += xchg<2>(x);
+  x += xchg<3>(x);
+  return sum_xor32(sum_xor16(x));
+}
+
+// KP waves share a row (slots 64*kp + lane), G row groups per workgroup, U
+// rows per group per step, two steps in flight.  grid.y = batch.
+template <int KP, int G, int U>
+__global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int kp = wv % KP;
+  const int grp = wv / KP;
+  const uint32_t nb = p.K / kQ4kBlockWeights;
+  const uint32_t s = 64u * kp + lane;  // this lane's slot
+  const bool has = s < 4u * nb;
+  // A lane without a slot reads slot 0 (valid memory) and contributes zero:
+  // its x values and their sums are zero.
+  const uint32_t blk = has ? s >> 2 : 0u, it = has ? s & 3u : 0u;
+  const uint32_t b = blockIdx.y;
+
+  [[maybe_unused]] __shared__ float red[G][U][KP];
+  const size_t row_bytes = (size_t)nb * kQ4kBlockBytes;
+  const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
+  const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
+  const uint32_t stride = gridDim.x * (G * U);
+
+  struct Rows {
+    u32x4 hd[U], qa[U], qb[U];
+  };
+  // Rows past the end re-read row N-1 and are not stored.
+  auto load = [&](Rows& r, uint32_t base) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t off = (size_t)min(base + grp * U + u, p.N - 1) * row_bytes;
+      r.hd[u] = ld16(whead + off);
+      r.qa[u] = ld16_stream(wslot + off);
+      r.qb[u] = ld16_stream(wslot + off + 16);
+    }
+  };
+  // The first step's weights are requested before x, so both latencies overlap.
+  Rows ra, rb;
+  uint32_t base = blockIdx.x * (G * U);
+  load(ra, base);
+
+  // This lane's 64 x values, kept in registers for the whole launch (read
+  // from L2: every wave of the grid reads x once).
+  const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
+  float xv[64];
+  const uint32_t xs0 = has ? s * 16 : 0u;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float4 t = xb[xs0 + j];
+    xv[4 * j] = has ? t.x : 0.f;
+    xv[4 * j + 1] = has ? t.y : 0.f;
+    xv[4 * j + 2] = has ? t.z : 0.f;
+    xv[4 * j + 3] = has ? t.w : 0.f;
+  }
+  float sxl = 0.f, sxh = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    sxl += xv[j];
+    sxh += xv[32 + j];
+  }
+
+  auto finish = [&](const Rows& r, uint32_t base) {
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      acc[u] = wave_sum(slot_dot(r.hd[u], r.qa[u], r.qb[u], 2 * it, xv, sxl, sxh));
+    const uint32_t r0 = base + grp * U;
+    if constexpr (KP == 1) {
+      if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t row = r0 + u;
+          if (row < p.N) {
+            float v = acc[u];
+            if (p.res) v += p.res[(size_t)b * p.N + row];
+            p.y[(size_t)b * p.N + row] = v;
+          }
+        }
+      }
+    } else {
+      if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) red[grp][u][kp] = acc[u];
+      }
+      __syncthreads();
+      if (kp == 0 && lane < U) {
+        const uint32_t row = r0 + lane;
+        if (row < p.N) {
+          float v = red[grp][lane][0];
+#pragma unroll
+          for (int k = 1; k < KP; ++k) v += red[grp][lane][k];
+          if (p.res) v += p.res[(size_t)b * p.N + row];
+          p.y[(size_t)b * p.N + row] = v;
+        }
+      }
+      __syncthreads();
+    }
+  };
+
+  // Two steps in flight: while one set of rows is reduced, the next loads.
+  // The loop bound is uniform over the workgroup (it depends on blockIdx
+  // only), as the barriers of the KP > 1 combine require.
+  for (; base < p.N; base += 2 * stride) {
+    load(rb, base + stride);
+    finish(ra, base);
+    load(ra, base + 2 * stride);
+    if (base + stride < p.N) finish(rb, base + stride);
+  }
+}
+
+// One thread per slot: the 64 weights of slot s of row n, rounded as the
+// shader rounds them (products and difference separately).
+__global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restrict__ w,
+                                                          float* __restrict__ out, uint32_t N,
+                                                          uint32_t K) {
+#pragma clang fp contract(off)
+  const uint32_t S = K / 64;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)N * S) return;
+  const uint32_t n = (uint32_t)(t / S), s = (uint32_t)(t % S);
+  const uint32_t blk = s >> 2, it = s & 3u;
+  const uint8_t* bp = w + ((size_t)n * (K / kQ4kBlockWeights) + blk) * kQ4kBlockBytes;
+  const u32x4 hd = ld16(bp), qa = ld16(bp + 16 + 32 * it), qb = ld16(bp + 32 + 32 * it);
+  const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+  uint32_t scl, mnl, sch, mnh;
+  scale_min(hd.y, hd.z, hd.w, 2 * it, scl, mnl);
+  scale_min(hd.y, hd.z, hd.w, 2 * it + 1, sch, mnh);
+  const float d1 = d * (float)scl, m1 = dmin * (float)mnl;
+  const float d2 = d * (float)sch, m2 = dmin * (float)mnh;
+  const uint32_t words[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  float* o = out + (size_t)n * K + (size_t)s * 64;
+#pragma unroll
+  for (int wd = 0; wd < 8; ++wd) {
+    float4 lo, hi;
+    const uint32_t q = words[wd];
+    lo.x = (float)(q & 0xFu) * d1 - m1;
+    lo.y = (float)((q >> 8) & 0xFu) * d1 - m1;
+    lo.z = (float)((q >> 16) & 0xFu) * d1 - m1;
+    lo.w = (float)((q >> 24) & 0xFu) * d1 - m1;
+    hi.x = (float)((q >> 4) & 0xFu) * d2 - m2;
+    hi.y = (float)((q >> 12) & 0xFu) * d2 - m2;
+    hi.z = (float)((q >> 20) & 0xFu) * d2 - m2;
+    hi.w = (float)((q >> 28) & 0xFu) * d2 - m2;
+    *reinterpret_cast<float4*>(o + 4 * wd) = lo;
+    *reinterpret_cast<float4*>(o + 32 + 4 * wd) = hi;
+  }
+}
+
+template <int KP>
+int launch_kp(const Q4kParams& p, hipStream_t stream) {
+  constexpr int G = KP == 1 ? 4 : (KP == 2 ? 2 : 1);
+  constexpr int U = 2;
+  // About one workgroup (four waves) per CU walking the rows: more waves
+  // only add reads of x and launch work (measured), fewer leave CUs idle.
+  const uint32_t cus = (uint32_t)device_cu_count();
+  const uint32_t steps = (p.N + G * U - 1) / (G * U);
+  const uint32_t wgs = std::max(1u, std::min(steps, cus * 4 / (KP * G)));
+  hipLaunchKernelGGL((q4k_matvec_kernel<KP, G, U>), dim3(wgs, p.B), dim3(64 * KP * G), 0, stream,
+                     p);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+}  // namespace
+
+int launch_q4k_matvec(const Q4kParams& p, hipStream_t stream) {
+  const uint32_t kp = (p.K / 64 + 63) / 64;
+  if (kp == 1) return launch_kp<1>(p, stream);
+  if (kp == 2) return launch_kp<2>(p, stream);
+  if (kp == 3) return launch_kp<3>(p, stream);
+  if (kp == 4) return launch_kp<4>(p, stream);
+  return fail(STS_ERR_INVALID, "K = %u too large (at most 16384)", p.K);
+}
+
+int launch_q4k_dequant(const uint8_t* w, float* out, uint32_t N, uint32_t K, hipStream_t stream) {
+  const uint64_t threads = (uint64_t)N * (K / 64);
+  const uint64_t wgs = (threads + 255) / 256;
+  if (wgs > 0x7FFFFFFFull) return fail(STS_ERR_INVALID, "matrix too large for one launch");
+  hipLaunchKernelGGL(q4k_dequant_kernel, dim3((uint32_t)wgs), dim3(256), 0, stream, w, out, N, K);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+}  // namespace sts

@@ -80,6 +80,8 @@ SIGNATURES = {
     "sts_kv_attend": (_int, [_vp, _vp, _vp, _f32, _vp]),
     "sts_kv_decode_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u64, _f32, _vp]),
     "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
+    "sts_q4k_matvec": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "sts_q4k_dequant": (_int, [_vp, _vp, _u32, _u32, _vp]),
 }
 
 _lib = None
@@ -422,3 +424,91 @@ def softmax_scale(head_dim: int) -> float:
     """head_dim^-0.5 as the reference computes it in f32 (model.rs:705)."""
     import numpy as np
     return float(np.float32(head_dim) ** np.float32(-0.5))
+
+
+# ---------------------------------------------------------------------------
+# Q4_K projections (gguf.rs:520-625, 808-905)
+# ---------------------------------------------------------------------------
+
+Q4K_BLOCK_BYTES = 144
+QK_K = 256
+
+
+class Q4KTensor:
+    """A Q4_K weight matrix [n, k] on the GPU, as Q4KTensor::from_q4k_bytes
+    (gguf.rs:530-563) holds it: the raw GGUF bytes, n*k/256 blocks of 144."""
+
+    def __init__(self, raw: torch.Tensor, shape: Sequence[int]):
+        n, k = int(shape[0]), int(shape[1])
+        if (n * k) % QK_K != 0:
+            raise StsError(STS_ERR_INVALID,
+                           f"Q4_K requires element count divisible by 256, got {n * k}")
+        expected = n * k // QK_K * Q4K_BLOCK_BYTES
+        if raw.dtype != torch.uint8 or raw.numel() != expected:
+            raise StsError(STS_ERR_INVALID, f"Q4_K byte count mismatch: expected {expected} "
+                           f"uint8 bytes for {n * k // QK_K} blocks, got {raw.numel()}")
+        self.raw = raw.contiguous()
+        self._shape = (n, k)
+
+    @classmethod
+    def from_q4k_bytes(cls, raw_bytes, shape: Sequence[int], device="cuda") -> "Q4KTensor":
+        t = torch.as_tensor(raw_bytes, dtype=torch.uint8).reshape(-1).to(device)
+        return cls(t, shape)
+
+    def shape(self):
+        return self._shape
+
+    def num_blocks(self) -> int:
+        return self._shape[0] * self._shape[1] // QK_K
+
+    def dequant(self, stream=None) -> torch.Tensor:
+        """[n, k] f32 weights, rounded as the reference shader computes them."""
+        n, k = self._shape
+        out = torch.empty((n, k), dtype=torch.float32, device=self.raw.device)
+        _check(load().sts_q4k_dequant(self.raw.data_ptr(), _ptr(out), k, n, _stream(stream)))
+        return out
+
+
+def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """q4k_matmul / q4k_matmul_with_residual for M = 1 (gguf.rs:808-905):
+    input [B, 1, K] (or [B, K]) -> [B, 1, N] = input @ W^T (+ residual)."""
+    n, k = weights.shape()
+    if input.shape[-1] != k:
+        raise StsError(STS_ERR_INVALID,
+                       f"K dimension mismatch: input has {input.shape[-1]}, weights have {k}")
+    if input.dim() == 3 and input.shape[1] != 1:
+        raise StsError(STS_ERR_INVALID, "only M = 1 (single-token) inputs are supported")
+    B = input.shape[0] if input.dim() >= 2 else 1
+    x = input.reshape(B, k).contiguous()
+    if out is None:
+        out = torch.empty((B, 1, n), dtype=torch.float32, device=input.device)
+    res = None
+    if residual is not None:
+        res = residual.reshape(B, n).contiguous()
+    _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out), B, k, n,
+                                 _stream(stream)))
+    return out
+
+
+def q4k_matmul_with_residual(input: torch.Tensor, weights: Q4KTensor, residual: torch.Tensor,
+                             stream=None) -> torch.Tensor:
+    """output = matmul(input, weights) + residual (gguf.rs:899-905), one launch."""
+    return q4k_matmul(input, weights, residual=residual, stream=stream)
+
+
+class Q4KLinear:
+    """Q4KLinear (gguf.rs:595-625): Q4_K weights with an optional f32 bias."""
+
+    def __init__(self, weights: Q4KTensor, bias: Optional[torch.Tensor] = None):
+        self.weights = weights
+        self.bias = bias
+
+    def forward(self, x: torch.Tensor, stream=None) -> torch.Tensor:
+        out = q4k_matmul(x, self.weights, stream=stream)
+        return out if self.bias is None else out + self.bias
+
+    def forward_with_residual(self, x: torch.Tensor, residual: torch.Tensor,
+                              stream=None) -> torch.Tensor:
+        out = q4k_matmul_with_residual(x, self.weights, residual, stream=stream)
+        return out if self.bias is None else out + self.bias

@@ -1,0 +1,114 @@
+"""Q4_K projections on the GPU against the oracle.
+
+Dequantisation is integer/byte work plus the shader's f32 products: bit-exact
+against the oracle.  The matvec sums in a different order than the shader
+(per lane, then across lanes), so it is checked against the f64 product and
+the shader-order oracle within the f32 rounding bound
+1e-5 * sum_k (|w_k| + 2 |dmin*min_k|) |x_k| (the scale of the terms any
+summation order adds up).  Shapes are the model's projections: temporal
+in_proj [12288, 4096], out_proj [4096, 4096], FFN linear_in [22528, 4096],
+linear_out [4096, 11264]; depformer in_proj [3072, 1024] and FFN linear_out
+[1024, 2816] (scripts/quantize.py:24-42).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sts_attn
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def bound(blocks, x, N):
+    K = x.shape[1]
+    w = oracle.q4k_dequant(blocks, N, K).astype(np.float64)
+    zq = blocks.reshape(-1, 144).copy()
+    zq[:, 16:] = 0
+    mins = -oracle.q4k_dequant(zq.reshape(-1), N, K).astype(np.float64)
+    return np.abs(x.astype(np.float64)) @ (np.abs(w) + 2 * np.abs(mins)).T
+
+
+@pytest.mark.parametrize("N,K", [(1, 256), (7, 512), (64, 4096), (4096, 4096), (33, 11264),
+                                 (3072, 1024), (5, 2816)])
+def test_dequant_bit_exact(gpu, N, K):
+    blocks = oracle.q4k_random_blocks(N * 31 + K, N, K)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    np.testing.assert_array_equal(host(w.dequant()), oracle.q4k_dequant(blocks, N, K))
+
+
+def test_dequant_of_quantized_weights(gpu):
+    """Blocks made by the reference's quantizer (scripts/quantize.py)."""
+    x = oracle.normal(3, (256, 4096)) * 0.02
+    blocks = oracle.q4k_quantize(x)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (256, 4096))
+    np.testing.assert_array_equal(host(w.dequant()), oracle.q4k_dequant(blocks, 256, 4096))
+
+
+@pytest.mark.parametrize("N,K,B", [(12288, 4096, 1), (4096, 4096, 1), (22528, 4096, 1),
+                                   (4096, 11264, 1), (3072, 1024, 1), (1024, 2816, 1),
+                                   (1001, 4096, 3), (5, 8192, 2), (17, 16384, 1), (1, 256, 1)])
+def test_matvec_against_oracle(gpu, N, K, B):
+    print(f"q4k matvec N={N} K={K} B={B}", flush=True)
+    blocks = oracle.q4k_random_blocks(N + K + B, N, K)
+    x = oracle.normal(N * 7 + B, (B, K))
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    got = host(sts_attn.q4k_matmul(dev(x[:, None, :]), w))[:, 0, :].astype(np.float64)
+    ref64 = oracle.q4k_matvec_f64(blocks, x, N)
+    tol = 1e-5 * bound(blocks, x, N)
+    assert (np.abs(got - ref64) <= tol).all(), np.abs(got - ref64).max()
+    if N * K <= 4096 * 4096:
+        refw = oracle.q4k_matvec_wgsl(blocks, x, N).astype(np.float64)
+        assert (np.abs(got - refw) <= tol).all()
+
+
+def test_matvec_with_residual_and_quantized_weights(gpu):
+    """q4k_matmul_with_residual on weights from the reference's quantizer."""
+    N, K = 4096, 4096
+    wf = oracle.normal(11, (N, K)) * 0.02
+    blocks = oracle.q4k_quantize(wf)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    x = oracle.normal(12, (1, 1, K))
+    res = oracle.normal(13, (1, 1, N))
+    got = host(sts_attn.q4k_matmul_with_residual(dev(x), w, dev(res)))[0, 0].astype(np.float64)
+    ref = oracle.q4k_matvec_f64(blocks, x[0], N)[0] + res[0, 0].astype(np.float64)
+    tol = 1e-5 * bound(blocks, x[0], N)[0] + 1e-6 * np.abs(res[0, 0])
+    assert (np.abs(got - ref) <= tol).all()
+    lin = sts_attn.Q4KLinear(w)
+    np.testing.assert_array_equal(host(lin.forward_with_residual(dev(x), dev(res))),
+                                  host(sts_attn.q4k_matmul_with_residual(dev(x), w, dev(res))))
+
+
+def test_matvec_bit_repeatable(gpu):
+    N, K = 12288, 4096
+    blocks = oracle.q4k_random_blocks(21, N, K)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    x = dev(oracle.normal(22, (1, 1, K)))
+    first = host(sts_attn.q4k_matmul(x, w))
+    for _ in range(5):
+        np.testing.assert_array_equal(host(sts_attn.q4k_matmul(x, w)), first)
+
+
+def test_matvec_argument_errors(gpu):
+    blocks = oracle.q4k_random_blocks(1, 4, 512)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (4, 512))
+    with pytest.raises(sts_attn.StsError):
+        sts_attn.q4k_matmul(dev(oracle.normal(1, (1, 1, 256))), w)  # K mismatch
+    lib = sts_attn.load()
+    x = dev(oracle.normal(2, (1, 512)))
+    y = torch.empty((1, 4), device="cuda")
+    assert lib.sts_q4k_matvec(w.raw.data_ptr(), x.data_ptr(), None, y.data_ptr(), 1, 384, 4,
+                              None) == sts_attn.STS_ERR_INVALID  # K not a multiple of 256
+    assert lib.sts_q4k_matvec(w.raw.data_ptr() + 4, x.data_ptr(), None, y.data_ptr(), 1, 512, 4,
+                              None) == sts_attn.STS_ERR_INVALID  # misaligned weights
+    with pytest.raises(sts_attn.StsError):
+        sts_attn.Q4KTensor.from_q4k_bytes(blocks[:-1], (4, 512))
