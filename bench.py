@@ -281,6 +281,7 @@ def bench_q4k(torch, sts, stream, steps, warmup):
            "weight_bytes_per_frame": w_bytes,
            "gbs": (w_bytes + io_bytes) / (us * 1e-6) / 1e9}
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
+    res["_layer0"] = layers[0]
     for name, (n, k) in (("linear_in", (22528, K)), ("linear_out", (K, 11264))):
         ws = [sts.Q4KTensor(q4k_random(torch, g, n, k), (n, k)) for _ in range(4)]
         xi = torch.randn((1, 1, k), generator=g, device="cuda")
@@ -296,6 +297,26 @@ def bench_q4k(torch, sts, stream, steps, warmup):
         res[name + "_gbs"] = n * k // 256 * 144 / (us_l * 1e-6) / 1e9
         del ws
     return res
+
+
+def cpu_baseline_q4k(torch, layer):
+    """The oracle's restatement of shader_q4k_matvec.wgsl on this host's cores:
+    layer 0's in_proj and out_proj (x0 of one frame), scaled to 24 layers."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    cores = min(os.cpu_count() or 1, 16)
+    oracle.set_num_threads(cores)
+    x = np.ascontiguousarray(np.random.default_rng(0).standard_normal((1, 4096)), np.float32)
+    wi, wo = (w.raw.cpu().numpy() for w in layer)
+    t0 = time.perf_counter()
+    for _ in range(2):
+        oracle.q4k_matvec_wgsl(wi, x, 3 * 4096)
+        oracle.q4k_matvec_wgsl(wo, x, 4096)
+    us_layer = (time.perf_counter() - t0) / 2 * 1e6
+    return {"value": us_layer * LAYERS, "unit": "us/frame", "cores": cores, "kind": "port",
+            "sample": "layer 0 in_proj + out_proj (2 runs), oracle shader-order f32 Q4_K "
+                      f"matvec, OpenMP over rows, scaled x{LAYERS}"}
 
 
 def cpu_baseline(torch, dec):
@@ -425,8 +446,15 @@ def main():
         line["ragged"] = {k: round(v, 2) for k, v in r.items()}
         line["ragged"]["frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     if "q4k" in extra:
+        q = extra["q4k"]
+        layer0 = q.pop("_layer0")
         line["q4k_projections"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                                   for k, v in extra["q4k"].items()}
+                                   for k, v in q.items()}
+        if not args.no_cpu:
+            log("bench: cpu baseline (q4k)")
+            cq = cpu_baseline_q4k(torch, layer0)
+            line["q4k_projections"]["cpu_baseline"] = cq
+            line["q4k_projections"]["gpu_vs_cpu"] = round(cq["value"] / q["us_per_frame"], 1)
     if cpu is not None:
         line["gpu_vs_cpu"] = round(cpu["value"] / dec["us_per_frame"], 1)
     print(json.dumps(line), flush=True)
