@@ -7,6 +7,7 @@ Inputs are regenerated at test time from the SplitMix64/Box-Muller spec
 (oracle.normal); each fixture stores the seeds, shapes, the SHA-256 of the
 generated inputs (so a changed generator is caught) and the expected outputs:
 `out_wgsl` (the shader's own f32 order) and `out_f64` (closed form in double).
+Q4_K cases also store their weight blocks and the dequantised weights.
 RoPE (theta 1e4, interleaved) is applied to Q and K at their logical
 positions, as the configs specify.
 """
@@ -51,6 +52,20 @@ def prefill_case(seed, H, D, M, cached, S, start):
                 input_sha=sha(q, kc, vc), out_wgsl=out_w, out_f64=out_d)
 
 
+def q4k_case(seed, N, K, B, quantized=False):
+    """Q4_K matvec: blocks from random bytes (every scale and quant pattern)
+    or from the reference's quantizer applied to normal data."""
+    if quantized:
+        blocks = oracle.q4k_quantize(oracle.normal(seed, (N, K)) * 0.05)
+    else:
+        blocks = oracle.q4k_random_blocks(seed, N, K)
+    x = oracle.normal(seed + 1, (B, K))
+    return dict(seed=seed, N=N, K=K, B=B, quantized=int(quantized), input_sha=sha(blocks, x),
+                blocks=blocks, dequant=oracle.q4k_dequant(blocks, N, K),
+                out_wgsl=oracle.q4k_matvec_wgsl(blocks, x, N),
+                out_f64=oracle.q4k_matvec_f64(blocks, x, N))
+
+
 CASES = {
     # BASELINE config 1: 1 layer, 32 x 128, L = 256, window at slot 0.
     "decode_config1": lambda: decode_case(101, 32, 128, 256, 256, 0),
@@ -64,6 +79,10 @@ CASES = {
     # Chunked prefill, small: 70 new rows after 45 cached, wrapped ring.
     "prefill_small": lambda: prefill_case(707, 1, 128, 128, 45, 70, 100),
     "prefill_small_d64": lambda: prefill_case(808, 2, 64, 100, 30, 33, 90),
+    # Q4_K projections: random blocks over three super-blocks per row, batch 2;
+    # and quantizer-made blocks.
+    "q4k_random": lambda: q4k_case(909, 6, 768, 2),
+    "q4k_quantized": lambda: q4k_case(1010, 4, 512, 1, quantized=True),
 }
 
 

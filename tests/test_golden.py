@@ -24,5 +24,13 @@ def test_fixture_reproduces(name):
     assert str(ref["input_sha"]) == new["input_sha"]
     np.testing.assert_array_equal(ref["out_wgsl"], new["out_wgsl"])
     np.testing.assert_allclose(ref["out_f64"], new["out_f64"], rtol=0, atol=1e-12)
-    # The two oracles agree with each other within f32 rounding.
-    assert np.abs(ref["out_wgsl"] - ref["out_f64"]).max() < 2e-6
+    if name.startswith("q4k"):
+        np.testing.assert_array_equal(ref["blocks"], new["blocks"])
+        np.testing.assert_array_equal(ref["dequant"], new["dequant"])
+        # f32 rounding of a K-term sum, relative to the terms' magnitude
+        # (|x| <= 4 for these seeds)
+        mag = np.abs(ref["dequant"]).sum(axis=1).max() * 4.0
+        assert np.abs(ref["out_wgsl"] - ref["out_f64"]).max() < 1e-5 * mag
+    else:
+        # The two oracles agree with each other within f32 rounding.
+        assert np.abs(ref["out_wgsl"] - ref["out_f64"]).max() < 2e-6

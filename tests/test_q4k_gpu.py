@@ -10,12 +10,15 @@ in_proj [12288, 4096], out_proj [4096, 4096], FFN linear_in [22528, 4096],
 linear_out [4096, 11264]; depformer in_proj [3072, 1024] and FFN linear_out
 [1024, 2816] (scripts/quantize.py:24-42).
 """
+import os
+
 import numpy as np
 import pytest
 import torch
 
 import oracle
 import sts_attn
+from conftest import GOLDEN
 
 pytestmark = pytest.mark.gpu
 
@@ -36,6 +39,19 @@ def bound(blocks, x, N):
     zq[:, 16:] = 0
     mins = -oracle.q4k_dequant(zq.reshape(-1), N, K).astype(np.float64)
     return np.abs(x.astype(np.float64)) @ (np.abs(w) + 2 * np.abs(mins)).T
+
+
+@pytest.mark.parametrize("name", ["q4k_random", "q4k_quantized"])
+def test_golden_fixtures(gpu, name):
+    f = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    N, K, B, seed = (int(f[k]) for k in ("N", "K", "B", "seed"))
+    x = oracle.normal(seed + 1, (B, K))
+    w = sts_attn.Q4KTensor.from_q4k_bytes(f["blocks"], (N, K))
+    np.testing.assert_array_equal(host(w.dequant()), f["dequant"])
+    got = host(sts_attn.q4k_matmul(dev(x[:, None, :]), w))[:, 0, :].astype(np.float64)
+    tol = 1e-5 * bound(f["blocks"], x, N)
+    assert (np.abs(got - f["out_f64"]) <= tol).all()
+    assert (np.abs(got - f["out_wgsl"]) <= tol).all()
 
 
 @pytest.mark.parametrize("N,K", [(1, 256), (7, 512), (64, 4096), (4096, 4096), (33, 11264),
