@@ -11,6 +11,9 @@
  *   RoPE                     model.rs:38-122
  *   prefill branch           model.rs:760-797, 837-873 (causal mask 539-563)
  *   depformer step attention depth.rs:79-273, depth_engine.rs:1121-1209
+ *   Q4_K matmul              gguf.rs:808-905   + wgsl/shader_q4k*.wgsl
+ *   depformer step chain     depth_engine.rs:884-1491 (RMSNorm, SwiGLU, Q4_0
+ *                            embeddings, top-k sampling)
  *
  * Conventions (every entry point):
  *   - Returns int status: STS_OK (0) on success, a negative STS_ERR_* code
@@ -288,6 +291,123 @@ int sts_q4k_matvec(const uint8_t* weights, const float* x, const float* residual
  * (shader_q4k_matvec.wgsl:117-136).
  */
 int sts_q4k_dequant(const uint8_t* weights, float* out, uint32_t k, uint32_t n, void* stream);
+
+/* ---- depformer step chain (depth_engine.rs:884-1491), batched over streams -
+ *
+ * The reference's DepthEngine runs one stream per frame as ~360 WGSL
+ * dispatches.  These entry points run B streams at once: every Q4_K product
+ * becomes a GEMM with the streams as rows, so each weight byte is read once
+ * per frame for the whole batch. */
+
+/*
+ * Y[m][n] = sum_k W[n][k] X[m][k] (+ residual[m][n]) for m < rows: the Q4_K
+ * product for more than one row, which the reference runs with the
+ * one-thread-per-output shader (q4k_matmul with M > 1, gguf.rs:810-897 and
+ * wgsl/shader_q4k.wgsl; q4k_matmul_with_residual, gguf.rs:899-905).  The
+ * weights are dequantised exactly as the shader rounds them and multiplied
+ * in f32 on the matrix cores.  With swiglu != 0 the matrix has n = 2F rows and
+ * y[m][j] = silu(G[m][j]) * G[m][j + F] for j < F (the SwiGLU of
+ * wgsl/shader_swiglu.wgsl applied to the product; residual must be NULL).
+ * k must be a multiple of 256 in 256..4096; x rows and weights 16-byte
+ * aligned; ldx, ldy, ldr are row strides in floats (ldx a multiple of 4).
+ */
+int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* residual,
+                 uint64_t ldr, float* y, uint64_t ldy, uint32_t rows, uint32_t k, uint32_t n,
+                 int swiglu, void* stream);
+
+/*
+ * RMSNorm of each row of x [rows][dim]: out = x * (1/sqrt(mean(x^2) + eps)) * alpha,
+ * summed in wgsl/shader_rmsnorm.wgsl's order (bit-identical results).
+ */
+int sts_rmsnorm(const float* x, const float* alpha, float* out, uint32_t rows, uint32_t dim,
+                float eps, void* stream);
+
+/*
+ * h[b][e] = proj[b][e] + E[token_b][e] for a Q4_0 embedding table E [vocab][dim]
+ * (wgsl/shader_embed_q4.wgsl + shader_vec_add.wgsl, depth_engine.rs:988-1057);
+ * token_b = tokens[b * tok_stride] (device), out-of-vocab tokens embed as zeros.
+ */
+int sts_embed_add_q4_0(const uint8_t* table, uint32_t vocab, const uint32_t* tokens,
+                       uint64_t tok_stride, const float* proj, float* h, uint32_t batch,
+                       uint32_t dim, void* stream);
+
+/*
+ * Top-k sampling with repetition penalty and temperature for each stream b
+ * (wgsl/shader_sample_topk.wgsl, depth_engine.rs:1411-1439): logits row b at
+ * logits + b*ld (not modified), rand[b*rs_stride] in [0,1),
+ * penalty tokens ptoks[b*pt_stride ..] (num_penalty[b*rs_stride] of them, at
+ * most 30), token to out[b*out_stride].  top_k <= 1 is the argmax.
+ * vocab <= 4096, top_k <= 256.  For distinct logits the draw equals the
+ * shader's; among equal logits this build ranks lower indices first.
+ */
+int sts_sample_topk(const float* logits, uint64_t ld, uint32_t batch, uint32_t vocab,
+                    uint32_t top_k, float temperature, float penalty, const float* rand,
+                    const uint32_t* ptoks, uint64_t pt_stride, const uint32_t* num_penalty,
+                    uint64_t rs_stride, uint32_t* out, uint64_t out_stride, void* stream);
+
+/* DepthEngineConfig (depth_engine.rs:50-107). */
+typedef struct sts_depformer_config {
+  uint32_t num_steps;       /* depth steps per frame (8)                       */
+  uint32_t num_layers;      /* 6                                               */
+  uint32_t dim;             /* 1024                                            */
+  uint32_t num_heads;       /* 16 (head_dim = dim / num_heads = 64)            */
+  uint32_t ffn;             /* 2816 (linear_in has 2*ffn rows)                 */
+  uint32_t temporal_dim;    /* 4096                                            */
+  uint32_t out_vocab;       /* 2048                                            */
+  uint32_t text_emb_vocab;  /* 32001                                           */
+  uint32_t audio_emb_vocab; /* 2049                                            */
+  uint32_t num_audio_emb;   /* audio tables; step s >= 1 reads min(s-1, n-1)   */
+  uint32_t kv_max_len;      /* 9 (>= num_steps)                                */
+  float rms_eps;            /* 1e-8                                            */
+  float attn_scale;         /* (dim / num_heads)^-0.5                          */
+} sts_depformer_config;
+
+/*
+ * Device pointers to the weights (LayerStepWeights / StepWeights,
+ * depth_engine.rs:114-175), owned by the caller for the handle's lifetime.
+ * Q4_K matrices: input_proj[step] [dim][temporal_dim]; attn_in_proj,
+ * attn_out_proj, ffn_linear_in, ffn_linear_out indexed [layer*num_steps + step],
+ * shapes [3 dim][dim], [dim][dim], [2 ffn][dim], [dim][ffn];
+ * output_linear[step] [out_vocab][dim].  f32 alphas per layer.  Q4_0 tables
+ * text_emb [text_emb_vocab][dim], audio_emb[i] [audio_emb_vocab][dim].  The
+ * pointer arrays themselves are host memory and are copied at create.
+ */
+typedef struct sts_depformer_weights {
+  const uint8_t* const* input_proj;
+  const uint8_t* const* attn_in_proj;
+  const uint8_t* const* attn_out_proj;
+  const uint8_t* const* ffn_linear_in;
+  const uint8_t* const* ffn_linear_out;
+  const float* const* norm1_alpha;
+  const float* const* norm2_alpha;
+  const uint8_t* const* output_linear;
+  const uint8_t* text_emb;
+  const uint8_t* const* audio_emb;
+} sts_depformer_weights;
+
+typedef struct sts_depformer sts_depformer;
+
+/* Validates the shapes, copies the weight pointers and allocates activations
+ * and KV caches for up to max_batch streams (DepthEngine::new). */
+int sts_depformer_create(const sts_depformer_config* cfg, const sts_depformer_weights* w,
+                         uint32_t max_batch, sts_depformer** out);
+int sts_depformer_destroy(sts_depformer* d);
+
+/*
+ * DepthEngine::generate (depth_engine.rs:884-1491) for `batch` streams:
+ * temporal_hidden [batch][temporal_dim], text_token [batch] (u32),
+ * rand [batch][num_steps], penalty_tokens [batch][num_steps][30],
+ * num_penalty [batch][num_steps] -> tokens [batch][num_steps]; optional
+ * logits [num_steps][batch][out_vocab] receives each step's logits before
+ * sampling.  All device pointers; nothing is read back, so the call can be
+ * captured in a HIP graph.  The KV caches start empty every call (the
+ * reference clears them per frame, depth_engine.rs:1497-1509).
+ */
+int sts_depformer_generate(sts_depformer* d, const float* temporal_hidden,
+                           const uint32_t* text_token, uint32_t batch, uint32_t top_k,
+                           float temperature, float penalty, const float* rand,
+                           const uint32_t* penalty_tokens, const uint32_t* num_penalty,
+                           uint32_t* tokens, float* logits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,23 @@ class KvState(ctypes.Structure):
         return (self.offset, self.len, self.write_pos, self.max_len)
 
 
+class DepformerCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "num_steps", "num_layers", "dim", "num_heads", "ffn", "temporal_dim", "out_vocab",
+        "text_emb_vocab", "audio_emb_vocab", "num_audio_emb", "kv_max_len")] + [
+        ("rms_eps", ctypes.c_float), ("attn_scale", ctypes.c_float)]
+
+
+_vpp = ctypes.POINTER(ctypes.c_void_p)
+
+
+class DepformerWeightPtrs(ctypes.Structure):
+    _fields_ = [("input_proj", _vpp), ("attn_in_proj", _vpp), ("attn_out_proj", _vpp),
+                ("ffn_linear_in", _vpp), ("ffn_linear_out", _vpp), ("norm1_alpha", _vpp),
+                ("norm2_alpha", _vpp), ("output_linear", _vpp), ("text_emb", ctypes.c_void_p),
+                ("audio_emb", _vpp)]
+
+
 def _load():
     if not os.path.exists(_LIB_PATH):
         raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run `make -C oracle`)")
@@ -64,6 +81,16 @@ def _load():
         "orc_q4k_quantize": (None, [_f32p, _u32, _u32, ctypes.c_void_p]),
         "orc_q4k_matvec_wgsl": (None, [ctypes.c_void_p, _f32p, _f32p, _u32, _u32, _u32]),
         "orc_q4k_matvec_f64": (None, [ctypes.c_void_p, _f32p, _f64p, _u32, _u32, _u32]),
+        "orc_rmsnorm_wgsl": (None, [_f32p, _f32p, _f32p, _u32, ctypes.c_float]),
+        "orc_swiglu": (None, [_f32p, _f32p, _u32]),
+        "orc_embed_q4_0": (None, [ctypes.c_void_p, _u32, _u32, _u32, _f32p]),
+        "orc_sample_topk_wgsl": (_u32, [_f32p, _u32, _u32, ctypes.c_float, ctypes.c_float,
+                                        ctypes.c_float, ctypes.POINTER(_u32), _u32]),
+        "orc_depformer_generate": (None, [ctypes.POINTER(DepformerCfg),
+                                          ctypes.POINTER(DepformerWeightPtrs), _f32p, _u32,
+                                          _u32, ctypes.c_float, ctypes.c_float, _f32p,
+                                          ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                                          ctypes.POINTER(_u32), _f32p, _f32p]),
         "orc_num_threads": (ctypes.c_int, []),
         "orc_set_num_threads": (None, [ctypes.c_int]),
     }
@@ -326,3 +353,164 @@ def q4k_random_blocks(seed, N, K):
         blk[:, off] = (half & 0xFF).astype(np.uint8)
         blk[:, off + 1] = (half >> 8).astype(np.uint8)
     return blk.reshape(-1)
+
+
+# ---- depformer step chain (depth_engine.rs:884-1491) ------------------------
+
+Q4_0_BLOCK_BYTES = 18
+
+
+def rmsnorm_wgsl(x, alpha, eps):
+    """shader_rmsnorm.wgsl on each row of x [R][D]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    a = np.ascontiguousarray(alpha, dtype=np.float32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        lib().orc_rmsnorm_wgsl(_p32(x[r]), _p32(a), _p32(out[r]), x.shape[1], float(eps))
+    return out
+
+
+def swiglu(gv):
+    """shader_swiglu.wgsl on each row of gv [R][2F] -> [R][F]."""
+    gv = np.ascontiguousarray(gv, dtype=np.float32)
+    F = gv.shape[1] // 2
+    out = np.empty((gv.shape[0], F), np.float32)
+    for r in range(gv.shape[0]):
+        lib().orc_swiglu(_p32(gv[r]), _p32(out[r]), F)
+    return out
+
+
+def embed_q4_0(table, vocab, dim, token):
+    t, tp = _u8(table)
+    assert t.size == vocab * dim // 32 * Q4_0_BLOCK_BYTES
+    out = np.empty(dim, np.float32)
+    lib().orc_embed_q4_0(tp, vocab, dim, int(token), _p32(out))
+    return out
+
+
+def sample_topk_wgsl(logits, top_k, temperature, penalty, rand, penalty_tokens=()):
+    """shader_sample_topk.wgsl on one row; returns (token, logits after penalty
+    and temperature)."""
+    lg = np.array(logits, dtype=np.float32, copy=True)
+    pt = np.ascontiguousarray(np.asarray(penalty_tokens, dtype=np.uint32).reshape(-1))
+    tok = lib().orc_sample_topk_wgsl(_p32(lg), lg.size, int(top_k), float(temperature),
+                                     float(penalty), float(rand),
+                                     pt.ctypes.data_as(ctypes.POINTER(_u32)), pt.size)
+    return int(tok), lg
+
+
+def q4_0_random_table(seed, vocab, dim, scale_lo=0x2000, scale_hi=0x2C00):
+    """Random Q4_0 embedding table [vocab][dim]: nibbles uniform, f16 scales
+    uniform over the bit patterns [scale_lo, scale_hi) (default ~0.008..0.06)."""
+    rng = np.random.default_rng(seed)
+    nb = vocab * dim // 32
+    blk = rng.integers(0, 256, size=(nb, Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    half = rng.integers(scale_lo, scale_hi, size=nb, dtype=np.uint16)
+    blk[:, 0] = (half & 0xFF).astype(np.uint8)
+    blk[:, 1] = (half >> 8).astype(np.uint8)
+    return blk.reshape(-1)
+
+
+class DepformerWeights:
+    """Host copies of a depformer's weights (numpy), in the layout of
+    orc_depformer_weights: Q4_K bytes per matrix, f32 alphas, Q4_0 tables."""
+
+    FIELDS = ("input_proj", "attn_in_proj", "attn_out_proj", "ffn_linear_in",
+              "ffn_linear_out", "norm1_alpha", "norm2_alpha", "output_linear", "audio_emb")
+
+    def __init__(self, cfg, **arrays):
+        self.cfg = dict(cfg)
+        for k, v in arrays.items():
+            setattr(self, k, v)
+
+    @classmethod
+    def synthetic(cls, cfg, seed=0, quantize=True):
+        """Weights ~ N(0, 1/K) per matrix, quantised with scripts/quantize.py's
+        scheme (quantize=True) or random Q4_K bytes scaled to the same size
+        (quantize=False, fast, for large shapes); alphas ~ 1 + N(0, 0.1^2)."""
+        c = cfg
+        S, L, D, F = c["num_steps"], c["num_layers"], c["dim"], c["ffn"]
+
+        def mat(tag, n, k):
+            if quantize:
+                w = normal(seed * 1000003 + tag, (n, k)) / np.float32(np.sqrt(k))
+                return q4k_quantize(w)
+            return _random_q4k_scaled(seed * 1000003 + tag, n, k)
+
+        tag = iter(range(1, 1 << 30))
+        w = dict(
+            input_proj=[mat(next(tag), D, c["temporal_dim"]) for _ in range(S)],
+            attn_in_proj=[mat(next(tag), 3 * D, D) for _ in range(L * S)],
+            attn_out_proj=[mat(next(tag), D, D) for _ in range(L * S)],
+            ffn_linear_in=[mat(next(tag), 2 * F, D) for _ in range(L * S)],
+            ffn_linear_out=[mat(next(tag), D, F) for _ in range(L * S)],
+            norm1_alpha=[(1 + 0.1 * normal(seed * 7 + 1 + l, (D,))).astype(np.float32)
+                         for l in range(L)],
+            norm2_alpha=[(1 + 0.1 * normal(seed * 7 + 101 + l, (D,))).astype(np.float32)
+                         for l in range(L)],
+            output_linear=[mat(next(tag), c["out_vocab"], D) for _ in range(S)],
+            text_emb=q4_0_random_table(seed * 13 + 1, c["text_emb_vocab"], D),
+            audio_emb=[q4_0_random_table(seed * 13 + 2 + i, c["audio_emb_vocab"], D)
+                       for i in range(c["num_audio_emb"])],
+        )
+        return cls(cfg, **w)
+
+
+def _random_q4k_scaled(seed, n, k):
+    """Random Q4_K bytes with d = dmin / 7.5 chosen so weights have mean ~0 and
+    standard deviation ~1/sqrt(k)."""
+    rng = np.random.default_rng(seed)
+    nb = n * k // QK_K
+    blk = rng.integers(0, 256, size=(nb, Q4K_BLOCK_BYTES), dtype=np.uint8)
+    # w = d*sc*q - dmin*m with sc, m ~ U[0,64), q ~ U[0,16): E[w] = 0 when
+    # dmin = 7.5 d; std(w) ~ 200 d.
+    d = np.float16(1.0 / (200.0 * np.sqrt(k)))
+    dm = np.float16(7.5 * float(d))
+    for off, v in ((0, d), (2, dm)):
+        bits = int(np.array(v, np.float16).view(np.uint16))
+        blk[:, off] = bits & 0xFF
+        blk[:, off + 1] = bits >> 8
+    return blk.reshape(-1)
+
+
+def _ptrs(arrs):
+    keep = [np.ascontiguousarray(a) for a in arrs]
+    arr = (ctypes.c_void_p * len(keep))(*[a.ctypes.data for a in keep])
+    return arr, keep
+
+
+def depformer_cfg_struct(cfg):
+    return DepformerCfg(**{f: cfg[f] for f, _ in DepformerCfg._fields_})
+
+
+def depformer_generate(weights, temporal_hidden, text_token, top_k, temperature, penalty,
+                       rand, penalty_tokens, num_penalty):
+    """orc_depformer_generate for one stream: returns (tokens [S], logits
+    [S][out_vocab], hidden [S][dim])."""
+    c = weights.cfg
+    S = c["num_steps"]
+    keep = []
+    fields = {}
+    for f in DepformerWeights.FIELDS:
+        arr, k = _ptrs(getattr(weights, f))
+        keep += k
+        fields[f] = ctypes.cast(arr, _vpp)
+        keep.append(arr)
+    te = np.ascontiguousarray(weights.text_emb)
+    keep.append(te)
+    wp = DepformerWeightPtrs(text_emb=te.ctypes.data, **fields)
+    cs = depformer_cfg_struct(c)
+    th = np.ascontiguousarray(temporal_hidden, dtype=np.float32).reshape(-1)
+    rd = np.ascontiguousarray(rand, dtype=np.float32).reshape(S)
+    pt = np.zeros((S, 30), np.uint32)
+    pt[:, :np.asarray(penalty_tokens).shape[-1]] = np.asarray(penalty_tokens, np.uint32).reshape(S, -1)[:, :30]
+    npn = np.ascontiguousarray(num_penalty, dtype=np.uint32).reshape(S)
+    tokens = np.empty(S, np.uint32)
+    logits = np.empty((S, c["out_vocab"]), np.float32)
+    hidden = np.empty((S, c["dim"]), np.float32)
+    u32p = ctypes.POINTER(_u32)
+    lib().orc_depformer_generate(ctypes.byref(cs), ctypes.byref(wp), _p32(th), int(text_token),
+                                 int(top_k), float(temperature), float(penalty), _p32(rd),
+                                 pt.ctypes.data_as(u32p), npn.ctypes.data_as(u32p),
+                                 tokens.ctypes.data_as(u32p), _p32(logits), _p32(hidden))
+    return tokens, logits, hidden

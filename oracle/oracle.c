@@ -566,6 +566,221 @@ void orc_q4k_matvec_f64(const uint8_t* blocks, const float* x, double* y, uint32
   free(w);
 }
 
+/* ---- depformer step chain -------------------------------------------------- */
+
+void orc_rmsnorm_wgsl(const float* x, const float* alpha, float* out, uint32_t D, float eps) {
+  float part[256];
+  for (uint32_t t = 0; t < 256; ++t) { /* shader_rmsnorm.wgsl:47-57 */
+    float acc = 0.f;
+    for (uint32_t i = t; i < D; i += 256) acc += x[i] * x[i];
+    part[t] = acc;
+  }
+  for (uint32_t half = 128; half >= 2; half >>= 1) /* :63-76 */
+    for (uint32_t t = 0; t < half; ++t) part[t] += part[t + half];
+  const float sum = part[0] + part[1];            /* :77 */
+  const float rms = sqrtf(sum / (float)D + eps);  /* :81 */
+  const float inv = 1.0f / rms;                   /* :82 */
+  for (uint32_t i = 0; i < D; ++i) out[i] = x[i] * inv * alpha[i]; /* :90 */
+}
+
+void orc_swiglu(const float* in, float* out, uint32_t F) {
+  for (uint32_t i = 0; i < F; ++i) {
+    const float gate = in[i], value = in[F + i];
+    out[i] = gate / (1.0f + expf(-gate)) * value; /* shader_swiglu.wgsl:30-34 */
+  }
+}
+
+/* shader_embed_q4.wgsl:34-56: an Inf/NaN scale reads as 0, otherwise exact. */
+static float q4_0_scale(uint16_t bits) {
+  if (((bits >> 10) & 0x1F) == 0x1F) return 0.f;
+  return orc_f16_to_f32(bits);
+}
+
+void orc_embed_q4_0(const uint8_t* table, uint32_t vocab, uint32_t dim, uint32_t token,
+                    float* out) {
+  if (token >= vocab) { /* :76-79 */
+    memset(out, 0, sizeof(float) * dim);
+    return;
+  }
+  const size_t row_bytes = (size_t)(dim / 32) * 18;
+  const uint8_t* row = table + (size_t)token * row_bytes;
+  for (uint32_t e = 0; e < dim; ++e) {
+    const uint8_t* blk = row + (e / 32) * 18; /* :82-87 */
+    const float scale = q4_0_scale(rd16(blk));
+    const uint32_t pos = e % 32;
+    const uint32_t nib = pos < 16 ? (blk[2 + pos] & 0xF) : (blk[2 + pos - 16] >> 4); /* :95-102 */
+    out[e] = ((float)nib - 8.0f) * scale; /* :105 */
+  }
+}
+
+uint32_t orc_sample_topk_wgsl(float* logits, uint32_t V, uint32_t top_k, float temperature,
+                              float penalty, float rand, const uint32_t* penalty_tokens,
+                              uint32_t num_penalty) {
+  /* Repetition penalty, shader_sample_topk.wgsl:56-69. */
+  for (uint32_t p = 0; p < num_penalty; ++p) {
+    const uint32_t tok = penalty_tokens[p];
+    int seen = 0;
+    for (uint32_t q = 0; q < p; ++q) seen |= penalty_tokens[q] == tok;
+    if (seen || tok >= V) continue;
+    const float val = logits[tok];
+    logits[tok] = val > 0.f ? val / penalty : val * penalty;
+  }
+  /* Temperature and per-lane maxima, :72-88 (lane t takes t, t+256, ...). */
+  float lmax[256];
+  uint32_t lidx[256];
+  for (uint32_t t = 0; t < 256; ++t) {
+    lmax[t] = -3.402823466e+38f;
+    lidx[t] = 0;
+  }
+  for (uint32_t i = 0; i < V; ++i) {
+    logits[i] = logits[i] / temperature;
+    const uint32_t t = i % 256;
+    if (logits[i] > lmax[t]) {
+      lmax[t] = logits[i];
+      lidx[t] = i;
+    }
+  }
+  for (uint32_t half = 128; half > 0; half >>= 1) /* :95-106 */
+    for (uint32_t t = 0; t < half; ++t)
+      if (lmax[t + half] > lmax[t]) {
+        lmax[t] = lmax[t + half];
+        lidx[t] = lidx[t + half];
+      }
+  if (top_k <= 1) return lidx[0]; /* :112-117 */
+
+  /* Thread 0's selection of the top K, :134-178. */
+  const uint32_t K = top_k;
+  float* vals = (float*)malloc(sizeof(float) * K);
+  uint32_t* idxs = (uint32_t*)malloc(sizeof(uint32_t) * K);
+  for (uint32_t j = 0; j < K; ++j) {
+    vals[j] = -3.402823466e+38f;
+    idxs[j] = 0;
+  }
+  const uint32_t first_k = K < V ? K : V;
+  for (uint32_t j = 0; j < first_k; ++j) {
+    vals[j] = logits[j];
+    idxs[j] = j;
+  }
+  float min_v = vals[0];
+  uint32_t min_p = 0;
+  for (uint32_t j = 1; j < first_k; ++j)
+    if (vals[j] < min_v) {
+      min_v = vals[j];
+      min_p = j;
+    }
+  for (uint32_t j = K; j < V; ++j) {
+    const float val = logits[j];
+    if (val > min_v) {
+      vals[min_p] = val;
+      idxs[min_p] = j;
+      min_v = vals[0];
+      min_p = 0;
+      for (uint32_t m = 1; m < K; ++m)
+        if (vals[m] < min_v) {
+          min_v = vals[m];
+          min_p = m;
+        }
+    }
+  }
+  /* Insertion sort, descending, :184-196. */
+  for (uint32_t si = 1; si < K; ++si) {
+    const float kv = vals[si];
+    const uint32_t ki = idxs[si];
+    int sj = (int)si - 1;
+    while (sj >= 0 && vals[sj] < kv) {
+      vals[sj + 1] = vals[sj];
+      idxs[sj + 1] = idxs[sj];
+      --sj;
+    }
+    vals[sj + 1] = kv;
+    idxs[sj + 1] = ki;
+  }
+  /* Softmax over the K and the cumulative draw, :198-221. */
+  float max_v = vals[0];
+  for (uint32_t j = 1; j < K; ++j)
+    if (vals[j] > max_v) max_v = vals[j];
+  float sum = 0.f;
+  for (uint32_t j = 0; j < K; ++j) {
+    vals[j] = expf(vals[j] - max_v);
+    sum = sum + vals[j];
+  }
+  float cum = 0.f;
+  uint32_t tok = idxs[K - 1];
+  for (uint32_t j = 0; j < K; ++j) {
+    cum = cum + vals[j] / sum;
+    if (rand < cum) {
+      tok = idxs[j];
+      break;
+    }
+  }
+  free(vals);
+  free(idxs);
+  return tok;
+}
+
+void orc_depformer_generate(const orc_depformer_cfg* c, const orc_depformer_weights* w,
+                            const float* temporal_hidden, uint32_t text_token, uint32_t top_k,
+                            float temperature, float penalty, const float* rand,
+                            const uint32_t* penalty_tokens, const uint32_t* num_penalty,
+                            uint32_t* tokens, float* logits_out, float* hidden_out) {
+  const uint32_t D = c->dim, H = c->num_heads, hd = c->dim / c->num_heads, M = c->kv_max_len;
+  const uint32_t F = c->ffn, S = c->num_steps;
+  float* proj = (float*)malloc(sizeof(float) * (size_t)S * D);
+  float* h = (float*)malloc(sizeof(float) * D);
+  float* h2 = (float*)malloc(sizeof(float) * D);
+  float* emb = (float*)malloc(sizeof(float) * D);
+  float* nrm = (float*)malloc(sizeof(float) * D);
+  float* qkv = (float*)malloc(sizeof(float) * 3 * D);
+  float* att = (float*)malloc(sizeof(float) * D);
+  float* gate = (float*)malloc(sizeof(float) * 2 * F);
+  float* sw = (float*)malloc(sizeof(float) * F);
+  float* logits = (float*)malloc(sizeof(float) * c->out_vocab);
+  float* kc = (float*)calloc((size_t)c->num_layers * H * M * hd, sizeof(float));
+  float* vc = (float*)calloc((size_t)c->num_layers * H * M * hd, sizeof(float));
+
+  /* Phase 1: projected[step] = input_proj[step] . temporal_hidden (:953-983). */
+  for (uint32_t st = 0; st < S; ++st)
+    orc_q4k_matvec_wgsl(w->input_proj[st], temporal_hidden, proj + (size_t)st * D, 1,
+                        c->temporal_dim, D);
+  uint32_t prev = text_token;
+  for (uint32_t st = 0; st < S; ++st) {
+    /* Embedding lookup and add (:988-1057). */
+    if (st == 0) {
+      orc_embed_q4_0(w->text_emb, c->text_emb_vocab, D, prev, emb);
+    } else {
+      const uint32_t e = st - 1 < c->num_audio_emb - 1 ? st - 1 : c->num_audio_emb - 1;
+      orc_embed_q4_0(w->audio_emb[e], c->audio_emb_vocab, D, prev, emb);
+    }
+    for (uint32_t i = 0; i < D; ++i) h[i] = proj[(size_t)st * D + i] + emb[i];
+    for (uint32_t l = 0; l < c->num_layers; ++l) {
+      const size_t wi = (size_t)l * S + st;
+      float* kl = kc + (size_t)l * H * M * hd;
+      float* vl = vc + (size_t)l * H * M * hd;
+      orc_rmsnorm_wgsl(h, w->norm1_alpha[l], nrm, D, c->rms_eps);          /* :1069-1095 */
+      orc_q4k_matvec_wgsl(w->attn_in_proj[wi], nrm, qkv, 1, D, 3 * D);     /* :1097-1119 */
+      orc_cache_write(qkv + D, kl, st, 1, 1, H, hd, M);                    /* :1121-1150 */
+      orc_cache_write(qkv + 2 * D, vl, st, 1, 1, H, hd, M);                /* :1152-1176 */
+      orc_attention_wgsl(qkv, kl, vl, att, H, hd, st + 1, c->attn_scale,
+                         (uint64_t)M * hd);                                /* :1178-1209 */
+      orc_q4k_matvec_wgsl(w->attn_out_proj[wi], att, h2, 1, D, D);         /* :1211-1233 */
+      for (uint32_t i = 0; i < D; ++i) h2[i] = h2[i] + h[i];               /* :1235-1257 */
+      orc_rmsnorm_wgsl(h2, w->norm2_alpha[l], nrm, D, c->rms_eps);         /* :1262-1282 */
+      orc_q4k_matvec_wgsl(w->ffn_linear_in[wi], nrm, gate, 1, D, 2 * F);   /* :1284-1306 */
+      orc_swiglu(gate, sw, F);                                             /* :1308-1332 */
+      orc_q4k_matvec_wgsl(w->ffn_linear_out[wi], sw, h, 1, F, D);          /* :1334-1356 */
+      for (uint32_t i = 0; i < D; ++i) h[i] = h[i] + h2[i];                /* :1358-1382 */
+    }
+    if (hidden_out) memcpy(hidden_out + (size_t)st * D, h, sizeof(float) * D);
+    orc_q4k_matvec_wgsl(w->output_linear[st], h, logits, 1, D, c->out_vocab); /* :1385-1409 */
+    if (logits_out) memcpy(logits_out + (size_t)st * c->out_vocab, logits, sizeof(float) * c->out_vocab);
+    prev = orc_sample_topk_wgsl(logits, c->out_vocab, top_k, temperature, penalty, rand[st],
+                                penalty_tokens + (size_t)st * 30, num_penalty[st]); /* :1411-1439 */
+    tokens[st] = prev;
+  }
+  free(proj); free(h); free(h2); free(emb); free(nrm); free(qkv); free(att);
+  free(gate); free(sw); free(logits); free(kc); free(vc);
+}
+
 int orc_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -152,6 +152,74 @@ void orc_q4k_matvec_wgsl(const uint8_t* blocks, const float* x, float* y, uint32
 void orc_q4k_matvec_f64(const uint8_t* blocks, const float* x, double* y, uint32_t B,
                         uint32_t K, uint32_t N);
 
+/* ---- depformer step chain (depth_engine.rs:884-1491) ---------------------- */
+
+/* shader_rmsnorm.wgsl:27-92 for one row of D: thread t (of 256) sums
+ * x[t]^2, x[t+256]^2, ... in order; tree sum (t += t+128, ..., then s0 + s1);
+ * rms = sqrt(sum / D + eps); out[i] = x[i] * (1 / rms) * alpha[i]. */
+void orc_rmsnorm_wgsl(const float* x, const float* alpha, float* out, uint32_t D, float eps);
+
+/* shader_swiglu.wgsl:24-35: out[i] = gate[i] / (1 + exp(-gate[i])) * value[i],
+ * gate = in[0..F), value = in[F..2F). */
+void orc_swiglu(const float* in, float* out, uint32_t F);
+
+/* shader_embed_q4.wgsl:58-107: row `token` of a Q4_0 table [vocab][dim]
+ * (18-byte blocks: f16 scale, 16 bytes of nibbles; element j < 16 is the low
+ * nibble of byte j, j >= 16 the high nibble of byte j-16; value
+ * (nibble - 8) * scale, an Inf/NaN scale reads as 0); zeros if
+ * token >= vocab. */
+void orc_embed_q4_0(const uint8_t* table, uint32_t vocab, uint32_t dim, uint32_t token,
+                    float* out);
+
+/* shader_sample_topk.wgsl:37-221 on one logits row (modified in place as the
+ * shader does): repetition penalty on the listed tokens (a token listed twice
+ * is penalised once: the shader's lanes read before they write), division by
+ * the temperature, then argmax (top_k <= 1) or top-k selection, insertion
+ * sort, softmax and the cumulative draw against `rand`.  Returns the token. */
+uint32_t orc_sample_topk_wgsl(float* logits, uint32_t V, uint32_t top_k, float temperature,
+                              float penalty, float rand, const uint32_t* penalty_tokens,
+                              uint32_t num_penalty);
+
+typedef struct orc_depformer_cfg {
+  uint32_t num_steps, num_layers, dim, num_heads, ffn, temporal_dim;
+  uint32_t out_vocab, text_emb_vocab, audio_emb_vocab, num_audio_emb, kv_max_len;
+  float rms_eps, attn_scale;
+} orc_depformer_cfg;
+
+/* Weights: Q4_K matrices (input_proj[step] [dim][temporal_dim];
+ * attn_in_proj, attn_out_proj, ffn_linear_in, ffn_linear_out indexed
+ * layer * num_steps + step, shapes [3 dim][dim], [dim][dim], [2 ffn][dim],
+ * [dim][ffn]; output_linear[step] [out_vocab][dim]), f32 norm alphas per
+ * layer, Q4_0 embeddings (text_emb, audio_emb[i]). */
+typedef struct orc_depformer_weights {
+  const uint8_t* const* input_proj;
+  const uint8_t* const* attn_in_proj;
+  const uint8_t* const* attn_out_proj;
+  const uint8_t* const* ffn_linear_in;
+  const uint8_t* const* ffn_linear_out;
+  const float* const* norm1_alpha;
+  const float* const* norm2_alpha;
+  const uint8_t* const* output_linear;
+  const uint8_t* text_emb;
+  const uint8_t* const* audio_emb;
+} orc_depformer_weights;
+
+/* DepthEngine::generate (depth_engine.rs:884-1491) for one stream, every op
+ * in its shader's f32 order: input projections of the temporal hidden state,
+ * then per step: embedding of the previous token (text_token at step 0,
+ * audio_emb[min(step-1, n-1)] after) added to the projection, num_layers
+ * blocks (rmsnorm, QKV projection, cache write at slot `step`, attention
+ * over slots 0..step, out_proj + residual, rmsnorm, linear_in, SwiGLU,
+ * linear_out + residual), output linear, top-k sampling.  rand
+ * [num_steps], penalty_tokens [num_steps][30], num_penalty [num_steps];
+ * tokens [num_steps].  logits [num_steps][out_vocab] (before sampling) and
+ * hidden [num_steps][dim] (input of the output linear) may be NULL. */
+void orc_depformer_generate(const orc_depformer_cfg* cfg, const orc_depformer_weights* w,
+                            const float* temporal_hidden, uint32_t text_token, uint32_t top_k,
+                            float temperature, float penalty, const float* rand,
+                            const uint32_t* penalty_tokens, const uint32_t* num_penalty,
+                            uint32_t* tokens, float* logits, float* hidden);
+
 /* Number of OpenMP threads the oracle uses (for the CPU-baseline record). */
 int orc_num_threads(void);
 void orc_set_num_threads(int n);

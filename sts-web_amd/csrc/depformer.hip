@@ -1,0 +1,420 @@
+// depformer.hip -- kernels of the depformer step chain for gfx950, batched over streams.
+//
+// The reference (crates/sts-wasm/src/depth_engine.rs:884-1491) runs one stream
+// per frame: per step an embedding lookup and add, six layers of RMSNorm,
+// Q4_K matvecs, cache writes, attention, SwiGLU and residual adds, then an
+// output matvec and top-k sampling, each a separate WGSL dispatch.  Here the
+// streams of a batch share every weight read: the Q4_K products become
+// GEMMs with the streams as the M dimension.
+//
+// q4k_gemm_kernel.  Workgroup = one 16-stream tile x all K: wave kb owns
+// super-block column kb (256 weights of every row) and keeps the 64 x values
+// of its lane in registers; the workgroup walks 16-row tiles.  Per tile a
+// wave dequantises the shader's f32 weights w = (d*scale)*q - dmin*min
+// (shader_q4k_matvec.wgsl:117-136, products and difference rounded
+// separately, so the weights are bit-identical) and feeds them to
+// v_mfma_f32_16x16x4f32: lane (r, g) supplies W[n0 + r][k] and X[m0 + r][k]
+// for k = 256 kb + 64 g + i at instruction i, g = lane / 16 being slot g of
+// the super-block (its 32 quant bytes, low nibbles sub-block 2g, high 2g+1).
+// The waves' partial tiles are summed through LDS in wave order
+// (deterministic), with the residual or the SwiGLU of a gate/value row pair
+// applied on the way out.
+#include <algorithm>
+#include <cfloat>
+#include <cstdint>
+
+#include "common.hpp"
+#include "depformer.hpp"
+#include "q4k.hpp"
+
+namespace sts {
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(1024) void q4k_gemm_kernel(const Q4kGemmParams p) {
+#pragma clang fp contract(off)
+  constexpr int NH = SWIGLU ? 2 : 1;
+  __shared__ float part[16][NH][256];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int kb = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t KB = p.K / kQ4kBlockWeights;  // waves in the workgroup
+  const uint32_t z = blockIdx.z, mt = blockIdx.y;
+  const uint8_t* W = p.w[z];
+  const float* X = p.x + z * p.x_zstride;
+  float* Y = p.y + z * p.y_zstride;
+
+  // x values of this lane: X[m][256 kb + 64 g + j], j < 64 (zero past M).
+  const uint32_t m = mt * 16 + r;
+  const bool m_ok = m < p.M;
+  const float4* xr =
+      reinterpret_cast<const float4*>(X + (size_t)(m_ok ? m : 0) * p.ldx + 256 * kb + 64 * g);
+  float xv[64];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float4 t = xr[j];
+    xv[4 * j] = m_ok ? t.x : 0.f;
+    xv[4 * j + 1] = m_ok ? t.y : 0.f;
+    xv[4 * j + 2] = m_ok ? t.z : 0.f;
+    xv[4 * j + 3] = m_ok ? t.w : 0.f;
+  }
+
+  const uint32_t nout = SWIGLU ? p.swiglu_f : p.N;
+  const uint32_t ntiles = (nout + 15) / 16;
+  const size_t row_bytes = (size_t)KB * kQ4kBlockBytes;
+  for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+#pragma unroll
+    for (int hv = 0; hv < NH; ++hv) {
+      // Rows past the end re-read row N-1; their outputs are not stored.
+      const uint32_t n = min(t * 16 + r + (hv ? p.swiglu_f : 0u), p.N - 1);
+      const uint8_t* blk = W + n * row_bytes + (size_t)kb * kQ4kBlockBytes;
+      const u32x4 hd = ld16(blk);
+      const u32x4 qa = ld16_stream(blk + 16 + 32 * g);
+      const u32x4 qb = ld16_stream(blk + 32 + 32 * g);
+      const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+      uint32_t scl, mnl, sch, mnh;
+      scale_min(hd.y, hd.z, hd.w, 2 * g, scl, mnl);
+      scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sch, mnh);
+      const float d1 = d * (float)scl, m1 = dmin * (float)mnl;
+      const float d2 = d * (float)sch, m2 = dmin * (float)mnh;
+      const uint32_t words[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+      floatx4 acc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        uint32_t lo = words[w] & 0x0F0F0F0Fu;
+        uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;
+        // Opaque to the optimiser, so each byte below is one v_cvt_f32_ubyte.
+        asm("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float wl = (float)((lo >> (8 * b)) & 0xFFu) * d1 - m1;
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(wl, xv[4 * w + b], acc[b], 0, 0, 0);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float wh = (float)((hi >> (8 * b)) & 0xFFu) * d2 - m2;
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(wh, xv[32 + 4 * w + b], acc[b], 0, 0, 0);
+        }
+      }
+      const floatx4 s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      // Accumulator element e of lane (r, g) is row 4g + e, stream r of the tile.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[kb][hv][(4 * g + e) * 16 + r] = s[e];
+    }
+    __syncthreads();
+    for (int o = tid; o < 256; o += blockDim.x) {
+      const uint32_t mo = mt * 16 + (o & 15), no = t * 16 + (o >> 4);
+      float v = part[0][0][o];
+      for (uint32_t w = 1; w < KB; ++w) v += part[w][0][o];
+      if constexpr (SWIGLU) {
+        float u = part[0][NH - 1][o];
+        for (uint32_t w = 1; w < KB; ++w) u += part[w][NH - 1][o];
+        v = v / (1.0f + expf(-v)) * u;
+      }
+      if (mo < p.M && no < nout) {
+        if (p.res) v += p.res[(size_t)mo * p.ldr + no];
+        Y[(size_t)mo * p.ldy + no] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// One workgroup of 256 per row, shader_rmsnorm.wgsl:27-92 step for step.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ alpha,
+                                                      float* __restrict__ out, uint32_t D,
+                                                      float eps) {
+#pragma clang fp contract(off)
+  __shared__ float sums[256];
+  const uint32_t t = threadIdx.x;
+  const float* xr = x + (size_t)blockIdx.x * D;
+  float* yr = out + (size_t)blockIdx.x * D;
+  float acc = 0.f;
+  for (uint32_t i = t; i < D; i += 256) acc += xr[i] * xr[i];
+  sums[t] = acc;
+  __syncthreads();
+  for (uint32_t half = 128; half >= 2; half >>= 1) {
+    if (t < half) sums[t] += sums[t + half];
+    __syncthreads();
+  }
+  const float total = sums[0] + sums[1];
+  const float rms = sqrtf(total / (float)D + eps);
+  const float inv = 1.0f / rms;
+  for (uint32_t i = t; i < D; i += 256) yr[i] = xr[i] * inv * alpha[i];
+}
+
+// shader_embed_q4.wgsl:58-107 fused with shader_vec_add.wgsl:20-28.
+__global__ __launch_bounds__(256) void embed_add_kernel(const uint8_t* __restrict__ table,
+                                                        uint32_t vocab,
+                                                        const uint32_t* __restrict__ tokens,
+                                                        uint64_t tok_stride,
+                                                        const float* __restrict__ proj,
+                                                        float* __restrict__ h, uint32_t D) {
+  const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t b = blockIdx.y;
+  if (e >= D) return;
+  const uint32_t tok = tokens[(size_t)b * tok_stride];
+  float emb = 0.f;
+  if (tok < vocab) {
+    const uint8_t* blk = table + ((size_t)tok * (D / 32) + e / 32) * 18;
+    const uint32_t bits = blk[0] | ((uint32_t)blk[1] << 8);
+    // An Inf/NaN scale reads as 0 (shader_embed_q4.wgsl:48-51).
+    const float scale = ((bits >> 10) & 0x1Fu) == 0x1Fu ? 0.f : half_bits_to_float(bits);
+    const uint32_t pos = e % 32;
+    const uint32_t nib = pos < 16 ? (blk[2 + pos] & 0xFu) : (blk[2 + pos - 16] >> 4);
+    emb = ((float)nib - 8.0f) * scale;
+  }
+  h[(size_t)b * D + e] = proj[(size_t)b * D + e] + emb;
+}
+
+// Monotone map of a float to a uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// shader_sample_topk.wgsl for one stream per workgroup.  Penalty, temperature
+// and the argmax follow the shader's lanes and tree exactly.  The top K are
+// found by a radix select of the K-th largest value and ranked by counting
+// (value descending, ties by index), which for distinct values is the
+// shader's selection and insertion sort; the softmax sum and the cumulative
+// draw run in the shader's sequential order on one lane.
+__global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) {
+  __shared__ float vals[kMaxVocab];
+  __shared__ float tv[256];
+  __shared__ uint32_t ti[256];
+  __shared__ uint32_t hist[256];
+  __shared__ float sv[kMaxTopK], ev[kMaxTopK];
+  __shared__ uint32_t si[kMaxTopK];
+  __shared__ float rv[kMaxTopK];
+  __shared__ uint32_t ri[kMaxTopK];
+  __shared__ uint32_t s_digit, s_rem, s_count, s_eq;
+  const uint32_t tid = threadIdx.x, b = blockIdx.x, V = p.V;
+  const float* lg = p.logits + (size_t)b * p.ld_logits;
+  for (uint32_t i = tid; i < V; i += 256) vals[i] = lg[i];
+  __syncthreads();
+
+  // Repetition penalty (:56-69); a token listed twice is penalised once.
+  const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
+  if (tid < np) {
+    const uint32_t* pt = p.ptoks + (size_t)b * p.pt_stride;
+    const uint32_t tok = pt[tid];
+    bool dup = false;
+    for (uint32_t q = 0; q < tid; ++q) dup |= pt[q] == tok;
+    if (!dup && tok < V) {
+      const float v = vals[tok];
+      vals[tok] = v > 0.f ? v / p.penalty : v * p.penalty;
+    }
+  }
+  __syncthreads();
+
+  // Temperature and per-lane maxima (:72-88), tree argmax (:95-106).
+  float lmax = -3.402823466e+38f;
+  uint32_t lidx = 0;
+  for (uint32_t i = tid; i < V; i += 256) {
+    const float v = vals[i] / p.temperature;
+    vals[i] = v;
+    if (v > lmax) {
+      lmax = v;
+      lidx = i;
+    }
+  }
+  tv[tid] = lmax;
+  ti[tid] = lidx;
+  __syncthreads();
+  for (uint32_t half = 128; half > 0; half >>= 1) {
+    if (tid < half && tv[tid + half] > tv[tid]) {
+      tv[tid] = tv[tid + half];
+      ti[tid] = ti[tid + half];
+    }
+    __syncthreads();
+  }
+  uint32_t* outp = p.out + (size_t)b * p.out_stride;
+  const uint32_t K = p.top_k;
+  if (K <= 1) {
+    if (tid == 0) *outp = ti[0];
+    return;
+  }
+
+  // Radix select of the Ks-th largest key, 8 bits at a time from the top.
+  const uint32_t Ks = min(K, V);
+  uint32_t prefix = 0, mask = 0, rem = Ks;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    hist[tid] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < V; i += 256) {
+      const uint32_t k = order_key(vals[i]);
+      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t cum = 0;
+      for (int d = 255; d >= 0; --d) {
+        const uint32_t c = hist[d];
+        if (cum + c >= rem) {
+          s_digit = (uint32_t)d;
+          s_rem = rem - cum;
+          break;
+        }
+        cum += c;
+      }
+    }
+    __syncthreads();
+    prefix |= s_digit << shift;
+    mask |= 0xFFu << shift;
+    rem = s_rem;
+  }
+  // Keys above the threshold are all taken; of those equal to it, `rem`.
+  if (tid == 0) {
+    s_count = 0;
+    s_eq = 0;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < V; i += 256) {
+    const uint32_t k = order_key(vals[i]);
+    if (k > prefix) {
+      const uint32_t slot = atomicAdd(&s_count, 1u);
+      sv[slot] = vals[i];
+      si[slot] = i;
+    } else if (k == prefix) {
+      atomicAdd(&s_eq, 1u);
+    }
+  }
+  __syncthreads();
+  if (s_eq == rem) {
+    for (uint32_t i = tid; i < V; i += 256)
+      if (order_key(vals[i]) == prefix) {
+        const uint32_t slot = atomicAdd(&s_count, 1u);
+        sv[slot] = vals[i];
+        si[slot] = i;
+      }
+  } else if (tid == 0) {
+    // Ties at the threshold: the lowest indices.
+    uint32_t c = s_count, take = rem;
+    for (uint32_t i = 0; i < V && take > 0; ++i)
+      if (order_key(vals[i]) == prefix) {
+        sv[c] = vals[i];
+        si[c] = i;
+        ++c;
+        --take;
+      }
+  }
+  __syncthreads();
+  // Rank by counting: value descending, index ascending.
+  if (tid < Ks) {
+    const float v = sv[tid];
+    const uint32_t ix = si[tid];
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < Ks; ++j) {
+      const float u = sv[j];
+      rank += (u > v) || (u == v && si[j] < ix);
+    }
+    rv[rank] = v;
+    ri[rank] = ix;
+  }
+  // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
+  for (uint32_t j = Ks + tid; j < K; j += 256) {
+    rv[j] = -3.402823466e+38f;
+    ri[j] = 0;
+  }
+  __syncthreads();
+  // Softmax over the K (:198-210) and the cumulative draw (:212-221).
+  const float max_v = rv[0];
+  for (uint32_t j = tid; j < K; j += 256) ev[j] = expf(rv[j] - max_v);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.f;
+    for (uint32_t j = 0; j < K; ++j) sum = sum + ev[j];
+    const float rnd = p.rand[(size_t)b * p.rs_stride];
+    float cum = 0.f;
+    uint32_t tok = ri[K - 1];
+    for (uint32_t j = 0; j < K; ++j) {
+      cum = cum + ev[j] / sum;
+      if (rnd < cum) {
+        tok = ri[j];
+        break;
+      }
+    }
+    *outp = tok;
+  }
+}
+
+}  // namespace
+
+int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
+  if (p.K % kQ4kBlockWeights != 0 || p.K == 0 || p.K > 16 * kQ4kBlockWeights)
+    return fail(STS_ERR_INVALID, "GEMM K = %u must be a multiple of 256 in 256..4096", p.K);
+  if (p.M == 0 || p.N == 0 || p.Z == 0 || p.Z > (uint32_t)kGemmMaxZ)
+    return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u Z=%u", p.M, p.N, p.Z);
+  if (p.swiglu_f && (p.swiglu_f * 2 != p.N))
+    return fail(STS_ERR_INVALID, "SwiGLU GEMM needs N = 2F (N=%u F=%u)", p.N, p.swiglu_f);
+  if (p.ldx % 4 != 0 || p.x_zstride % 4 != 0 || (reinterpret_cast<uintptr_t>(p.x) & 15))
+    return fail(STS_ERR_INVALID, "GEMM x rows must be 16-byte aligned");
+  for (uint32_t z = 0; z < p.Z; ++z)
+    if (!p.w[z] || (reinterpret_cast<uintptr_t>(p.w[z]) & 15))
+      return fail(STS_ERR_INVALID, "GEMM weights %u null or not 16-byte aligned", z);
+  const uint32_t KB = p.K / kQ4kBlockWeights;
+  const uint32_t mtiles = (p.M + 15) / 16;
+  const uint32_t nout = p.swiglu_f ? p.swiglu_f : p.N;
+  const uint32_t ntiles = (nout + 15) / 16;
+  // About 2 workgroups per CU in total; each walks ntiles / gx row tiles and
+  // reads its 16 x rows once.
+  const uint32_t cus = (uint32_t)device_cu_count();
+  const uint32_t gx = std::max(1u, std::min(ntiles, 2 * cus / std::max(1u, mtiles * p.Z)));
+  if (mtiles > 65535u) return fail(STS_ERR_INVALID, "M = %u too large", p.M);
+  const dim3 grid(gx, mtiles, p.Z), block(64 * KB);
+  if (p.swiglu_f)
+    hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, block, 0, stream, p);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+int launch_rmsnorm(const float* x, const float* alpha, float* out, uint32_t rows, uint32_t D,
+                   float eps, hipStream_t stream) {
+  if (rows == 0 || D == 0) return fail(STS_ERR_INVALID, "empty RMSNorm");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, alpha, out, D, eps);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+int launch_embed_add(const uint8_t* table, uint32_t vocab, const uint32_t* tokens,
+                     uint64_t tok_stride, const float* proj, float* h, uint32_t B, uint32_t D,
+                     hipStream_t stream) {
+  if (D % 32 != 0 || B == 0 || B > 65535u)
+    return fail(STS_ERR_INVALID, "embedding: dim %u must be a multiple of 32, batch %u", D, B);
+  hipLaunchKernelGGL(embed_add_kernel, dim3((D + 255) / 256, B), dim3(256), 0, stream, table,
+                     vocab, tokens, tok_stride, proj, h, D);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+int launch_sample_topk(const SampleParams& p, hipStream_t stream) {
+  if (p.V == 0 || p.V > kMaxVocab)
+    return fail(STS_ERR_INVALID, "sampling vocab %u must be in 1..%u", p.V, kMaxVocab);
+  if (p.top_k > kMaxTopK)
+    return fail(STS_ERR_INVALID, "top_k %u exceeds %u", p.top_k, kMaxTopK);
+  if (p.B == 0) return STS_OK;
+  hipLaunchKernelGGL(sample_topk_kernel, dim3(p.B), dim3(256), 0, stream, p);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+}  // namespace sts

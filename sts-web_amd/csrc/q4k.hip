@@ -42,26 +42,6 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
-// Exact binary16 -> binary32 (v_cvt_f32_f16), as WGSL unpack2x16float.
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
-  return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xFFFFu));
-}
-
-// 6-bit scale and min of sub-block j from the packed scale bytes held in
-// s0 (bytes 0-3), s1 (4-7), s2 (8-11); shader_q4k_matvec.wgsl:85-113.
-__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j,
-                                          uint32_t& sc, uint32_t& mn) {
-  const uint32_t sh = 8u * (j & 3u);
-  const uint32_t b0 = (s0 >> sh) & 0xFFu, b1 = (s1 >> sh) & 0xFFu, b2 = (s2 >> sh) & 0xFFu;
-  if (j < 4) {
-    sc = b0 & 63u;
-    mn = b1 & 63u;
-  } else {
-    sc = (b2 & 0xFu) | ((b0 >> 6) << 4);
-    mn = (b2 >> 4) | ((b1 >> 6) << 4);
-  }
-}
-
 // d1*sum(q_lo*x_lo) - m1*sum(x_lo) + d2*sum(q_hi*x_hi) - m2*sum(x_hi) for one slot.
 __device__ __forceinline__ float slot_dot(u32x4 hd, u32x4 qa, u32x4 qb, uint32_t jl,
                                           const float (&xv)[64], float sxl, float sxh) {

@@ -82,6 +82,15 @@ SIGNATURES = {
     "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
     "sts_q4k_matvec": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "sts_q4k_dequant": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "sts_q4k_gemm": (_int, [_vp, _vp, _u64, _vp, _u64, _vp, _u64, _u32, _u32, _u32, _int, _vp]),
+    "sts_rmsnorm": (_int, [_vp, _vp, _vp, _u32, _u32, _f32, _vp]),
+    "sts_embed_add_q4_0": (_int, [_vp, _u32, _vp, _u64, _vp, _vp, _u32, _u32, _vp]),
+    "sts_sample_topk": (_int, [_vp, _u64, _u32, _u32, _u32, _f32, _f32, _vp, _vp, _u64, _vp,
+                               _u64, _vp, _u64, _vp]),
+    "sts_depformer_create": (_int, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
+    "sts_depformer_destroy": (_int, [_vp]),
+    "sts_depformer_generate": (_int, [_vp, _vp, _vp, _u32, _u32, _f32, _f32, _vp, _vp, _vp, _vp,
+                                      _vp, _vp]),
 }
 
 _lib = None
@@ -471,23 +480,28 @@ class Q4KTensor:
 
 def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch.Tensor] = None,
                out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """q4k_matmul / q4k_matmul_with_residual for M = 1 (gguf.rs:808-905):
-    input [B, 1, K] (or [B, K]) -> [B, 1, N] = input @ W^T (+ residual)."""
+    """q4k_matmul / q4k_matmul_with_residual (gguf.rs:808-905): input
+    [B, M, K] (or [B, K]) -> [B, M, N] = input @ W^T (+ residual).  M = 1 runs
+    the matvec (the reference's single-token path), M > 1 the GEMM (its
+    prefill path)."""
     n, k = weights.shape()
     if input.shape[-1] != k:
         raise StsError(STS_ERR_INVALID,
                        f"K dimension mismatch: input has {input.shape[-1]}, weights have {k}")
-    if input.dim() == 3 and input.shape[1] != 1:
-        raise StsError(STS_ERR_INVALID, "only M = 1 (single-token) inputs are supported")
     B = input.shape[0] if input.dim() >= 2 else 1
-    x = input.reshape(B, k).contiguous()
+    Mrows = input.shape[1] if input.dim() == 3 else 1
+    x = input.reshape(B * Mrows, k).contiguous()
     if out is None:
-        out = torch.empty((B, 1, n), dtype=torch.float32, device=input.device)
+        out = torch.empty((B, Mrows, n), dtype=torch.float32, device=input.device)
     res = None
     if residual is not None:
-        res = residual.reshape(B, n).contiguous()
-    _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out), B, k, n,
-                                 _stream(stream)))
+        res = residual.reshape(B * Mrows, n).contiguous()
+    if Mrows == 1:
+        _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out), B, k,
+                                     n, _stream(stream)))
+    else:
+        _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, _ptr(res), n, _ptr(out), n,
+                                   B * Mrows, k, n, 0, _stream(stream)))
     return out
 
 
@@ -512,3 +526,148 @@ class Q4KLinear:
                               stream=None) -> torch.Tensor:
         out = q4k_matmul_with_residual(x, self.weights, residual, stream=stream)
         return out if self.bias is None else out + self.bias
+
+
+# ---------------------------------------------------------------------------
+# Depformer step chain (depth_engine.rs:884-1491), batched over streams
+# ---------------------------------------------------------------------------
+
+def q4k_gemm(x: torch.Tensor, weights: Q4KTensor, residual: Optional[torch.Tensor] = None,
+             swiglu: bool = False, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """x [R, K] -> [R, N] = x @ W^T (+ residual); with swiglu, W has 2F rows and
+    the result is silu(G[:, :F]) * G[:, F:] ([R, F])."""
+    n, k = weights.shape()
+    R = x.shape[0]
+    x = x.reshape(R, k).contiguous()
+    nout = n // 2 if swiglu else n
+    if out is None:
+        out = torch.empty((R, nout), dtype=torch.float32, device=x.device)
+    res = residual.reshape(R, n).contiguous() if residual is not None else None
+    _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, _ptr(res), n, _ptr(out), nout,
+                               R, k, n, 1 if swiglu else 0, _stream(stream)))
+    return out
+
+
+def rmsnorm(x: torch.Tensor, alpha: torch.Tensor, eps: float,
+            out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """shader_rmsnorm.wgsl on every row of x [..., D]."""
+    D = x.shape[-1]
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load().sts_rmsnorm(_ptr(x), _ptr(alpha.contiguous()), _ptr(out), x.numel() // D, D,
+                              eps, _stream(stream)))
+    return out
+
+
+def embed_add_q4_0(table: torch.Tensor, vocab: int, tokens: torch.Tensor, proj: torch.Tensor,
+                   out: Optional[torch.Tensor] = None, tok_stride: int = 1,
+                   stream=None) -> torch.Tensor:
+    """proj [B, D] + the Q4_0 embedding rows of tokens (uint32 device tensor)."""
+    B, D = proj.shape
+    if out is None:
+        out = torch.empty_like(proj)
+    _check(load().sts_embed_add_q4_0(table.data_ptr(), vocab, tokens.data_ptr(), tok_stride,
+                                     _ptr(proj.contiguous()), _ptr(out), B, D, _stream(stream)))
+    return out
+
+
+def sample_top_k(logits: torch.Tensor, top_k: int, temperature: float, penalty: float,
+                 rand: torch.Tensor, penalty_tokens: torch.Tensor, num_penalty: torch.Tensor,
+                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """shader_sample_topk.wgsl for each row of logits [B, V]: rand [B] f32,
+    penalty_tokens [B, 30] and num_penalty [B] uint32 -> tokens [B] uint32."""
+    B, V = logits.shape
+    if out is None:
+        out = torch.empty(B, dtype=torch.uint32, device=logits.device)
+    _check(load().sts_sample_topk(_ptr(logits.contiguous()), V, B, V, top_k, temperature,
+                                  penalty, _ptr(rand), penalty_tokens.data_ptr(),
+                                  penalty_tokens.stride(0), num_penalty.data_ptr(), 1,
+                                  out.data_ptr(), 1, _stream(stream)))
+    return out
+
+
+class DepformerConfig(ctypes.Structure):
+    """DepthEngineConfig (depth_engine.rs:50-107)."""
+    _fields_ = [(n, _u32) for n in (
+        "num_steps", "num_layers", "dim", "num_heads", "ffn", "temporal_dim", "out_vocab",
+        "text_emb_vocab", "audio_emb_vocab", "num_audio_emb", "kv_max_len")] + [
+        ("rms_eps", _f32), ("attn_scale", _f32)]
+
+    @classmethod
+    def personaplex(cls, num_steps: int = 8) -> "DepformerConfig":
+        """DepthEngineConfig::from_sts_config of the default StsConfig
+        (lib.rs:123-170, depth_engine.rs:86-107)."""
+        return cls(num_steps=num_steps, num_layers=6, dim=1024, num_heads=16, ffn=2816,
+                   temporal_dim=4096, out_vocab=2048, text_emb_vocab=32001,
+                   audio_emb_vocab=2049, num_audio_emb=15, kv_max_len=9, rms_eps=1e-8,
+                   attn_scale=float((1024 / 16) ** -0.5))
+
+
+_vpp = ctypes.POINTER(_vp)
+
+
+class DepformerWeightPtrs(ctypes.Structure):
+    _fields_ = [("input_proj", _vpp), ("attn_in_proj", _vpp), ("attn_out_proj", _vpp),
+                ("ffn_linear_in", _vpp), ("ffn_linear_out", _vpp), ("norm1_alpha", _vpp),
+                ("norm2_alpha", _vpp), ("output_linear", _vpp), ("text_emb", _vp),
+                ("audio_emb", _vpp)]
+
+
+class DepthEngine:
+    """DepthEngine (depth_engine.rs:177-1510) for a batch of streams.
+
+    `weights` maps each field of sts_depformer_weights to device tensors:
+    uint8 Q4_K/Q4_0 bytes for the matrices and tables (lists, indexed as the
+    header documents), float32 alphas per layer.  The tensors must outlive the
+    engine."""
+
+    LIST_FIELDS = ("input_proj", "attn_in_proj", "attn_out_proj", "ffn_linear_in",
+                   "ffn_linear_out", "norm1_alpha", "norm2_alpha", "output_linear", "audio_emb")
+
+    def __init__(self, config: DepformerConfig, weights: dict, max_batch: int):
+        self.config = config
+        self.max_batch = max_batch
+        self._weights = weights
+        arrays = {}
+        self._keep = []
+        for f in self.LIST_FIELDS:
+            arr = (_vp * len(weights[f]))(*[t.data_ptr() for t in weights[f]])
+            self._keep.append(arr)
+            arrays[f] = ctypes.cast(arr, _vpp)
+        wp = DepformerWeightPtrs(text_emb=weights["text_emb"].data_ptr(), **arrays)
+        h = _vp()
+        _check(load().sts_depformer_create(ctypes.byref(config), ctypes.byref(wp), max_batch,
+                                           ctypes.byref(h)))
+        self._h = h
+
+    def generate(self, temporal_hidden: torch.Tensor, text_token: torch.Tensor, audio_temp: float,
+                 audio_top_k: int, audio_penalty: float, rand: torch.Tensor,
+                 penalty_tokens: torch.Tensor, num_penalty: torch.Tensor,
+                 tokens: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None,
+                 stream=None) -> torch.Tensor:
+        """DepthEngine::generate (depth_engine.rs:884-1441) for B streams:
+        temporal_hidden [B, temporal_dim], text_token [B] uint32, rand
+        [B, num_steps] f32, penalty_tokens [B, num_steps, 30] and num_penalty
+        [B, num_steps] uint32 -> tokens [B, num_steps] uint32 (on the device,
+        not read back).  logits, if given, [num_steps, B, out_vocab] f32."""
+        B = temporal_hidden.shape[0]
+        S = self.config.num_steps
+        if tokens is None:
+            tokens = torch.empty((B, S), dtype=torch.uint32, device=temporal_hidden.device)
+        _check(load().sts_depformer_generate(
+            self._h, _ptr(temporal_hidden.contiguous()), text_token.data_ptr(), B, audio_top_k,
+            audio_temp, audio_penalty, _ptr(rand), penalty_tokens.data_ptr(),
+            num_penalty.data_ptr(), tokens.data_ptr(), _ptr(logits), _stream(stream)))
+        return tokens
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _check(load().sts_depformer_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

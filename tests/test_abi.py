@@ -184,3 +184,39 @@ def test_counters_match_oracle_over_random_walk(M):
         assert (s.offset, s.len, s.write_pos) == (o.offset, o.len, o.write_pos)
         start, ln = c.window()
         assert ln == o.len and start == o.window_start() and 0 <= start < M
+
+
+def test_depformer_chain_argument_errors():
+    """Rejected before any device work (no GPU needed)."""
+    lib = sts_attn.load()
+    assert "multiple of 256" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1000, None, 0, FAKE, 3072, 64,
+                                                      1000, 3072, 0, None))
+    assert "SwiGLU" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, FAKE, 5632, FAKE, 2816, 64, 1024,
+                                             5632, 1, None))
+    assert "strides" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 512, None, 0, FAKE, 3072, 64, 1024,
+                                              3072, 0, None))
+    assert "null" in _err(lib.sts_rmsnorm(None, FAKE, FAKE, 4, 1024, 1e-8, None))
+    assert "eps" in _err(lib.sts_rmsnorm(FAKE, FAKE, FAKE, 4, 1024, float("nan"), None))
+    assert "multiple of 32" in _err(lib.sts_embed_add_q4_0(FAKE, 10, FAKE, 1, FAKE, FAKE, 2, 100,
+                                                          None))
+    assert "vocab" in _err(lib.sts_sample_topk(FAKE, 5000, 2, 5000, 10, 1.0, 1.0, FAKE, FAKE, 30,
+                                               FAKE, 1, FAKE, 1, None))
+    assert "top_k" in _err(lib.sts_sample_topk(FAKE, 2048, 2, 2048, 257, 1.0, 1.0, FAKE, FAKE, 30,
+                                               FAKE, 1, FAKE, 1, None))
+    assert "temperature" in _err(lib.sts_sample_topk(FAKE, 2048, 2, 2048, 5, 0.0, 1.0, FAKE, FAKE,
+                                                     30, FAKE, 1, FAKE, 1, None))
+    cfg = sts_attn.DepformerConfig.personaplex()
+    cfg.num_heads = 12  # head_dim 85
+    h = ctypes.c_void_p()
+    w = sts_attn.DepformerWeightPtrs()
+    assert "bad layers" in _err(lib.sts_depformer_create(ctypes.byref(cfg), ctypes.byref(w), 4,
+                                                          ctypes.byref(h)))
+    cfg = sts_attn.DepformerConfig.personaplex()
+    cfg.kv_max_len = 4
+    assert "kv_max_len" in _err(lib.sts_depformer_create(ctypes.byref(cfg), ctypes.byref(w), 4,
+                                                          ctypes.byref(h)))
+    cfg = sts_attn.DepformerConfig.personaplex()
+    assert "null weight" in _err(lib.sts_depformer_create(ctypes.byref(cfg), ctypes.byref(w), 4,
+                                                           ctypes.byref(h)))
+    assert "null" in _err(lib.sts_depformer_generate(None, FAKE, FAKE, 1, 1, 1.0, 1.0, FAKE, FAKE,
+                                                     FAKE, FAKE, None, None))
