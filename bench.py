@@ -9,7 +9,8 @@ beyond the 256 MB MALL).  Inputs are resident in HBM before timing.
 Also reported (extra fields): decode without the append (sts_kv_attend),
 chunked prefill (config 3, f32 and bf16-MFMA), depformer frame (config 4),
 ragged multi-stream decode (config 5), the Q4_K projections around attention
-(in_proj / out_proj per frame, FFN shapes); and the CPU baseline -- the oracle's
+(in_proj / out_proj per frame, FFN shapes), the whole depformer step chain for
+64 streams (depth_engine.rs:884-1491); and the CPU baseline -- the oracle's
 restatement of the reference shader, timed on this host's cores on a bounded
 sample of the same workload.
 
@@ -299,6 +300,116 @@ def bench_q4k(torch, sts, stream, steps, warmup):
     return res
 
 
+DEPF_STREAMS = 64
+
+
+def q4k_random_scaled(torch, g, n, k):
+    """Random Q4_K bytes with d = 1/(200 sqrt k) and dmin = 7.5 d, so weights
+    have mean ~0 and standard deviation ~1/sqrt(k) (activations stay O(1)
+    through the depformer's layers)."""
+    import numpy as np
+    nb = n * k // 256
+    raw = torch.randint(0, 256, (nb, 144), generator=g, device="cuda", dtype=torch.uint8)
+    d = np.float16(1.0 / (200.0 * np.sqrt(k)))
+    for off, v in ((0, d), (2, np.float16(7.5 * float(d)))):
+        bits = int(np.array(v, np.float16).view(np.uint16))
+        raw[:, off] = bits & 0xFF
+        raw[:, off + 1] = bits >> 8
+    return raw.reshape(-1)
+
+
+def q4_0_random(torch, g, vocab, dim):
+    """Random Q4_0 table: nibbles uniform, f16 scales in ~[0.008, 0.06)."""
+    nb = vocab * dim // 32
+    raw = torch.randint(0, 256, (nb, 18), generator=g, device="cuda", dtype=torch.uint8)
+    half = torch.randint(0x2000, 0x2C00, (nb,), generator=g, device="cuda", dtype=torch.int32)
+    raw[:, 0] = (half & 0xFF).to(torch.uint8)
+    raw[:, 1] = (half >> 8).to(torch.uint8)
+    return raw.reshape(-1)
+
+
+def bench_depformer_frame(torch, sts, stream, steps, warmup):
+    """The whole depformer step chain (depth_engine.rs:884-1491) at the
+    PersonaPlex shapes for 64 streams: 8 steps x 6 layers with per-step Q4_K
+    weights (375 MB), replayed from a HIP graph."""
+    cfg = sts.DepformerConfig.personaplex()
+    S, L, D, F, V, T = (cfg.num_steps, cfg.num_layers, cfg.dim, cfg.ffn, cfg.out_vocab,
+                        cfg.temporal_dim)
+    B = DEPF_STREAMS
+    g = torch.Generator(device="cuda").manual_seed(8)
+    mat = lambda n, k: q4k_random_scaled(torch, g, n, k)
+    w = {"input_proj": [mat(D, T) for _ in range(S)],
+         "attn_in_proj": [mat(3 * D, D) for _ in range(L * S)],
+         "attn_out_proj": [mat(D, D) for _ in range(L * S)],
+         "ffn_linear_in": [mat(2 * F, D) for _ in range(L * S)],
+         "ffn_linear_out": [mat(D, F) for _ in range(L * S)],
+         "norm1_alpha": [1 + 0.1 * torch.randn(D, generator=g, device="cuda") for _ in range(L)],
+         "norm2_alpha": [1 + 0.1 * torch.randn(D, generator=g, device="cuda") for _ in range(L)],
+         "output_linear": [mat(V, D) for _ in range(S)],
+         "text_emb": q4_0_random(torch, g, cfg.text_emb_vocab, D),
+         "audio_emb": [q4_0_random(torch, g, cfg.audio_emb_vocab, D)
+                       for _ in range(cfg.num_audio_emb)]}
+    eng = sts.DepthEngine(cfg, w, max_batch=B)
+    th = torch.randn((B, T), generator=g, device="cuda")
+    text = torch.randint(0, cfg.text_emb_vocab, (B,), generator=g, device="cuda",
+                         dtype=torch.int32)
+    rand = torch.rand((B, S), generator=g, device="cuda")
+    pt = torch.randint(0, V, (B, S, 30), generator=g, device="cuda", dtype=torch.int32)
+    npn = torch.randint(0, 31, (B, S), generator=g, device="cuda", dtype=torch.int32)
+    tokens = torch.empty((B, S), dtype=torch.int32, device="cuda")
+    args = (th, text, 0.8, 250, 1.2, rand, pt, npn)
+
+    def frame():
+        eng.generate(*args, tokens=tokens, stream=stream)
+
+    for _ in range(warmup):
+        frame()
+    with Timer(torch, stream) as te:
+        for _ in range(steps):
+            frame()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        frame()
+    for _ in range(warmup):
+        graph.replay()
+    with Timer(torch, stream) as tg:
+        for _ in range(steps):
+            graph.replay()
+    us = tg.ms * 1e3 / steps
+    weights = S * (D * T + V * D) + L * S * (3 * D * D + D * D + 2 * F * D + D * F)
+    flops = 2 * B * weights
+    res = {"streams": B, "us_per_frame": us, "eager_us_per_frame": te.ms * 1e3 / steps,
+           "tokens_per_s": B * S / (us * 1e-6),
+           "launches_per_frame": 1 + S * (1 + 5 * L + 2),
+           "gemm_flops_per_frame": flops, "gemm_tflops": flops / (us * 1e-6) / 1e12,
+           "weight_bytes_per_frame": weights // 256 * 144}
+    res["frac_of_fp32_peak"] = res["gemm_tflops"] / FP32_PEAK_TFLOPS
+    res["_cpu"] = (cfg, w, args)
+    return res
+
+
+def cpu_baseline_depformer_frame(torch, cfg, w, args):
+    """The oracle's restatement of the chain (every op in its shader's f32
+    order) for stream 0 of the benchmarked frame, scaled to the 64 streams."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    cores = min(os.cpu_count() or 1, 16)
+    oracle.set_num_threads(cores)
+    c = {f: getattr(cfg, f) for f, _ in cfg._fields_}
+    host = {f: [t.cpu().numpy() for t in w[f]] for f in oracle.DepformerWeights.FIELDS}
+    ow = oracle.DepformerWeights(c, text_emb=w["text_emb"].cpu().numpy(), **host)
+    th, text, temp, top_k, pen, rand, pt, npn = args
+    t0 = time.perf_counter()
+    oracle.depformer_generate(ow, th[0].cpu().numpy(), int(text[0]), top_k, temp, pen,
+                              rand[0].cpu().numpy(), pt[0].cpu().numpy().view(np.uint32),
+                              npn[0].cpu().numpy().view(np.uint32))
+    us = (time.perf_counter() - t0) * 1e6
+    return {"value": us * DEPF_STREAMS, "unit": "us/frame", "cores": cores, "kind": "port",
+            "sample": f"stream 0 of the frame (1 run), oracle shader-order f32 chain, "
+                      f"OpenMP inside each op, scaled x{DEPF_STREAMS}"}
+
+
 def cpu_baseline_q4k(torch, layer):
     """The oracle's restatement of shader_q4k_matvec.wgsl on this host's cores:
     layer 0's in_proj and out_proj (x0 of one frame), scaled to 24 layers."""
@@ -398,6 +509,11 @@ def main():
         if want("q4k"):
             log("bench: q4k projections")
             extra["q4k"] = bench_q4k(torch, sts, stream, args.steps, args.warmup)
+        if want("depformer_frame"):
+            log("bench: depformer frame (64 streams)")
+            extra["depformer_frame"] = bench_depformer_frame(torch, sts, stream,
+                                                             max(3, args.steps // 2),
+                                                             min(args.warmup, 2))
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
@@ -455,6 +571,16 @@ def main():
             cq = cpu_baseline_q4k(torch, layer0)
             line["q4k_projections"]["cpu_baseline"] = cq
             line["q4k_projections"]["gpu_vs_cpu"] = round(cq["value"] / q["us_per_frame"], 1)
+    if "depformer_frame" in extra:
+        f = extra["depformer_frame"]
+        cfg_w_args = f.pop("_cpu")
+        line["depformer_frame"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                   for k, v in f.items()}
+        if not args.no_cpu:
+            log("bench: cpu baseline (depformer frame)")
+            cf = cpu_baseline_depformer_frame(torch, *cfg_w_args)
+            line["depformer_frame"]["cpu_baseline"] = cf
+            line["depformer_frame"]["gpu_vs_cpu"] = round(cf["value"] / f["us_per_frame"], 1)
     if cpu is not None:
         line["gpu_vs_cpu"] = round(cpu["value"] / dec["us_per_frame"], 1)
     print(json.dumps(line), flush=True)

@@ -308,12 +308,17 @@ int sts_q4k_dequant(const uint8_t* weights, float* out, uint32_t k, uint32_t n, 
  * in f32 on the matrix cores.  With swiglu != 0 the matrix has n = 2F rows and
  * y[m][j] = silu(G[m][j]) * G[m][j + F] for j < F (the SwiGLU of
  * wgsl/shader_swiglu.wgsl applied to the product; residual must be NULL).
- * k must be a multiple of 256 in 256..4096; x rows and weights 16-byte
- * aligned; ldx, ldy, ldr are row strides in floats (ldx a multiple of 4).
+ * With norm_alpha non-NULL each x row is first RMS-normalised,
+ * x * (1/sqrt(mean(x^2) + norm_eps)) * norm_alpha (the RMSNorm that precedes
+ * every projection of the depformer, depth_engine.rs:1069-1095, 1262-1282,
+ * fused; its sum of squares is taken in this kernel's order, not the
+ * shader's).  k must be a multiple of 256 in 256..4096; x rows, norm_alpha
+ * and weights 16-byte aligned; ldx, ldy, ldr are row strides in floats (ldx a
+ * multiple of 4).
  */
-int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* residual,
-                 uint64_t ldr, float* y, uint64_t ldy, uint32_t rows, uint32_t k, uint32_t n,
-                 int swiglu, void* stream);
+int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* norm_alpha,
+                 float norm_eps, const float* residual, uint64_t ldr, float* y, uint64_t ldy,
+                 uint32_t rows, uint32_t k, uint32_t n, int swiglu, void* stream);
 
 /*
  * RMSNorm of each row of x [rows][dim]: out = x * (1/sqrt(mean(x^2) + eps)) * alpha,
@@ -337,8 +342,11 @@ int sts_embed_add_q4_0(const uint8_t* table, uint32_t vocab, const uint32_t* tok
  * logits + b*ld (not modified), rand[b*rs_stride] in [0,1),
  * penalty tokens ptoks[b*pt_stride ..] (num_penalty[b*rs_stride] of them, at
  * most 30), token to out[b*out_stride].  top_k <= 1 is the argmax.
- * vocab <= 4096, top_k <= 256.  For distinct logits the draw equals the
- * shader's; among equal logits this build ranks lower indices first.
+ * vocab <= 4096, top_k <= 256.  The top k and their order equal the
+ * shader's for distinct logits (among equal logits this build ranks lower
+ * indices first); the softmax sum and running total are summed in a
+ * different f32 order, so the draw can differ only where rand lies within
+ * rounding of a cumulative boundary.
  */
 int sts_sample_topk(const float* logits, uint64_t ld, uint32_t batch, uint32_t vocab,
                     uint32_t top_k, float temperature, float penalty, const float* rand,

@@ -41,11 +41,20 @@ __device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-template <bool SWIGLU>
-__global__ __launch_bounds__(1024) void q4k_gemm_kernel(const Q4kGemmParams p) {
+// The 48 weight bytes lane (r, g) needs of one super-block row: header and
+// the 32 quant bytes of slot g.
+struct WTile {
+  u32x4 hd, qa, qb;
+};
+
+// MAXT: the largest workgroup (64 * K/256 threads) the instance runs with;
+// 256 (K <= 1024) leaves the register file to the prefetch buffers.
+template <bool SWIGLU, int MAXT>
+__global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
 #pragma clang fp contract(off)
   constexpr int NH = SWIGLU ? 2 : 1;
   __shared__ float part[16][NH][256];
+  __shared__ float ssq[16][16];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int kb = tid >> 6;
@@ -55,6 +64,26 @@ __global__ __launch_bounds__(1024) void q4k_gemm_kernel(const Q4kGemmParams p) {
   const uint8_t* W = p.w[z];
   const float* X = p.x + z * p.x_zstride;
   float* Y = p.y + z * p.y_zstride;
+  const uint32_t nout = SWIGLU ? p.swiglu_f : p.N;
+  const uint32_t ntiles = (nout + 15) / 16;
+  const size_t row_bytes = (size_t)KB * kQ4kBlockBytes;
+
+  // Rows past the end (and tiles past the last) re-read valid rows; their
+  // outputs are not stored.
+  auto load_w = [&](WTile (&wt)[NH], uint32_t t) {
+    t = min(t, ntiles - 1);
+#pragma unroll
+    for (int hv = 0; hv < NH; ++hv) {
+      const uint32_t n = min(t * 16 + r + (hv ? p.swiglu_f : 0u), p.N - 1);
+      const uint8_t* blk = W + n * row_bytes + (size_t)kb * kQ4kBlockBytes;
+      wt[hv].hd = ld16(blk);
+      wt[hv].qa = ld16_stream(blk + 16 + 32 * g);
+      wt[hv].qb = ld16_stream(blk + 32 + 32 * g);
+    }
+  };
+  // The first tile's weights are requested before x, so both latencies overlap.
+  WTile cur[NH], nxt[NH];
+  load_w(cur, blockIdx.x);
 
   // x values of this lane: X[m][256 kb + 64 g + j], j < 64 (zero past M).
   const uint32_t m = mt * 16 + r;
@@ -70,19 +99,35 @@ __global__ __launch_bounds__(1024) void q4k_gemm_kernel(const Q4kGemmParams p) {
     xv[4 * j + 2] = m_ok ? t.z : 0.f;
     xv[4 * j + 3] = m_ok ? t.w : 0.f;
   }
+  if (p.norm_alpha) {
+    // RMSNorm of the 16 rows (shader_rmsnorm.wgsl:80-90): x * (1/rms) * alpha,
+    // with the sum of squares taken over this workgroup's registers.
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) q += xv[j] * xv[j];
+    q += __shfl_xor(q, 16, 64);
+    q += __shfl_xor(q, 32, 64);
+    if (g == 0) ssq[kb][r] = q;
+    __syncthreads();
+    float tot = ssq[0][r];
+    for (uint32_t w = 1; w < KB; ++w) tot += ssq[w][r];
+    const float inv = 1.0f / sqrtf(tot / (float)p.K + p.norm_eps);
+    const float4* al = reinterpret_cast<const float4*>(p.norm_alpha + 256 * kb + 64 * g);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float4 a = al[j];
+      xv[4 * j] = xv[4 * j] * inv * a.x;
+      xv[4 * j + 1] = xv[4 * j + 1] * inv * a.y;
+      xv[4 * j + 2] = xv[4 * j + 2] * inv * a.z;
+      xv[4 * j + 3] = xv[4 * j + 3] * inv * a.w;
+    }
+  }
 
-  const uint32_t nout = SWIGLU ? p.swiglu_f : p.N;
-  const uint32_t ntiles = (nout + 15) / 16;
-  const size_t row_bytes = (size_t)KB * kQ4kBlockBytes;
   for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    load_w(nxt, t + gridDim.x);  // next tile in flight during this one
 #pragma unroll
     for (int hv = 0; hv < NH; ++hv) {
-      // Rows past the end re-read row N-1; their outputs are not stored.
-      const uint32_t n = min(t * 16 + r + (hv ? p.swiglu_f : 0u), p.N - 1);
-      const uint8_t* blk = W + n * row_bytes + (size_t)kb * kQ4kBlockBytes;
-      const u32x4 hd = ld16(blk);
-      const u32x4 qa = ld16_stream(blk + 16 + 32 * g);
-      const u32x4 qb = ld16_stream(blk + 32 + 32 * g);
+      const u32x4 hd = cur[hv].hd, qa = cur[hv].qa, qb = cur[hv].qb;
       const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
       uint32_t scl, mnl, sch, mnh;
       scale_min(hd.y, hd.z, hd.w, 2 * g, scl, mnl);
@@ -131,6 +176,8 @@ __global__ __launch_bounds__(1024) void q4k_gemm_kernel(const Q4kGemmParams p) {
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int hv = 0; hv < NH; ++hv) cur[hv] = nxt[hv];
   }
 }
 
@@ -192,8 +239,8 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 // and the argmax follow the shader's lanes and tree exactly.  The top K are
 // found by a radix select of the K-th largest value and ranked by counting
 // (value descending, ties by index), which for distinct values is the
-// shader's selection and insertion sort; the softmax sum and the cumulative
-// draw run in the shader's sequential order on one lane.
+// shader's selection and insertion sort; the softmax values are the shader's
+// (exp of v - max), their sum and running total come from a wave scan.
 __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) {
   __shared__ float vals[kMaxVocab];
   __shared__ float tv[256];
@@ -204,6 +251,8 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   __shared__ float rv[kMaxTopK];
   __shared__ uint32_t ri[kMaxTopK];
   __shared__ uint32_t s_digit, s_rem, s_count, s_eq;
+  __shared__ uint32_t s_ptok[kMaxPenalty];
+  __shared__ uint64_t ck[kMaxTopK];
   const uint32_t tid = threadIdx.x, b = blockIdx.x, V = p.V;
   const float* lg = p.logits + (size_t)b * p.ld_logits;
   for (uint32_t i = tid; i < V; i += 256) vals[i] = lg[i];
@@ -211,11 +260,12 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
 
   // Repetition penalty (:56-69); a token listed twice is penalised once.
   const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
+  if (tid < np) s_ptok[tid] = p.ptoks[(size_t)b * p.pt_stride + tid];
+  __syncthreads();
   if (tid < np) {
-    const uint32_t* pt = p.ptoks + (size_t)b * p.pt_stride;
-    const uint32_t tok = pt[tid];
+    const uint32_t tok = s_ptok[tid];
     bool dup = false;
-    for (uint32_t q = 0; q < tid; ++q) dup |= pt[q] == tok;
+    for (uint32_t q = 0; q < tid; ++q) dup |= s_ptok[q] == tok;
     if (!dup && tok < V) {
       const float v = vals[tok];
       vals[tok] = v > 0.f ? v / p.penalty : v * p.penalty;
@@ -263,16 +313,30 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
       if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 0xFFu], 1u);
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t cum = 0;
-      for (int d = 255; d >= 0; --d) {
-        const uint32_t c = hist[d];
-        if (cum + c >= rem) {
-          s_digit = (uint32_t)d;
-          s_rem = rem - cum;
-          break;
+    if (tid < 64) {
+      // Wave 0 picks the digit: lane l holds bins 4l..4l+3; a suffix sum over
+      // lanes finds the lane whose bins straddle the rem-th largest key.
+      const uint32_t h0 = hist[4 * tid], h1 = hist[4 * tid + 1], h2 = hist[4 * tid + 2],
+                     h3 = hist[4 * tid + 3];
+      uint32_t suf = h0 + h1 + h2 + h3;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t v = __shfl_down(suf, off, 64);
+        if (tid + off < 64) suf += v;
+      }
+      uint32_t above = __shfl_down(suf, 1, 64);  // keys in higher lanes' bins
+      if (tid == 63) above = 0;
+      if (suf >= rem && above < rem) {
+        const uint32_t hb[4] = {h0, h1, h2, h3};
+        uint32_t cum = above;
+        for (int d = 3; d >= 0; --d) {
+          if (cum + hb[d] >= rem) {
+            s_digit = 4 * tid + d;
+            s_rem = rem - cum;
+            break;
+          }
+          cum += hb[d];
         }
-        cum += c;
       }
     }
     __syncthreads();
@@ -316,17 +380,24 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
       }
   }
   __syncthreads();
-  // Rank by counting: value descending, index ascending.
+  // Rank by counting: value descending, index ascending, as one 64-bit key
+  // (order key above, complemented index below) so the count is branch-free.
+  if (tid < Ks) ck[tid] = ((uint64_t)order_key(sv[tid]) << 32) | (0xFFFFFFFFu - si[tid]);
+  __syncthreads();
   if (tid < Ks) {
-    const float v = sv[tid];
-    const uint32_t ix = si[tid];
+    const uint64_t mine = ck[tid];
     uint32_t rank = 0;
-    for (uint32_t j = 0; j < Ks; ++j) {
-      const float u = sv[j];
-      rank += (u > v) || (u == v && si[j] < ix);
+    uint32_t j = 0;
+    for (; j + 8 <= Ks; j += 8) {
+      uint64_t c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = ck[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) rank += c[u] > mine ? 1u : 0u;
     }
-    rv[rank] = v;
-    ri[rank] = ix;
+    for (; j < Ks; ++j) rank += ck[j] > mine ? 1u : 0u;
+    rv[rank] = sv[tid];
+    ri[rank] = si[tid];
   }
   // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
   for (uint32_t j = Ks + tid; j < K; j += 256) {
@@ -338,20 +409,43 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   const float max_v = rv[0];
   for (uint32_t j = tid; j < K; j += 256) ev[j] = expf(rv[j] - max_v);
   __syncthreads();
-  if (tid == 0) {
-    float sum = 0.f;
-    for (uint32_t j = 0; j < K; ++j) sum = sum + ev[j];
-    const float rnd = p.rand[(size_t)b * p.rs_stride];
-    float cum = 0.f;
-    uint32_t tok = ri[K - 1];
-    for (uint32_t j = 0; j < K; ++j) {
-      cum = cum + ev[j] / sum;
-      if (rnd < cum) {
-        tok = ri[j];
-        break;
-      }
+  if (tid < 64) {
+    // Wave 0: lane l holds values 4l..4l+3.  The sum and the running total
+    // are formed by a wave scan rather than the shader's single-lane loop, a
+    // different f32 order: the draw can differ only where rand lies within
+    // rounding of a cumulative boundary.
+    float e[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) e[c] = 4 * tid + c < K ? ev[4 * tid + c] : 0.f;
+    float sum = (e[0] + e[1]) + (e[2] + e[3]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    float q[4], run = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      run += e[c] / sum;
+      q[c] = run;  // inclusive prefix within the lane
     }
-    *outp = tok;
+    // Exclusive prefix of the lane totals.
+    float pre = run;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float v = __shfl_up(pre, off, 64);
+      if (tid >= off) pre += v;
+    }
+    pre -= run;
+    const float rnd = p.rand[(size_t)b * p.rs_stride];
+    int first = 4;
+#pragma unroll
+    for (int c = 3; c >= 0; --c)
+      if (4 * tid + c < K && rnd < pre + q[c]) first = c;
+    const uint64_t hits = __ballot(first < 4);
+    uint32_t pick = K - 1;
+    if (hits) {
+      const int lane0 = __builtin_ctzll(hits);
+      pick = 4 * lane0 + __shfl(first, lane0, 64);
+    }
+    if (tid == 0) *outp = ri[pick];
   }
 }
 
@@ -373,16 +467,23 @@ int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
   const uint32_t mtiles = (p.M + 15) / 16;
   const uint32_t nout = p.swiglu_f ? p.swiglu_f : p.N;
   const uint32_t ntiles = (nout + 15) / 16;
-  // About 2 workgroups per CU in total; each walks ntiles / gx row tiles and
+  // Up to 4 workgroups per CU in total; each walks ntiles / gx row tiles and
   // reads its 16 x rows once.
   const uint32_t cus = (uint32_t)device_cu_count();
-  const uint32_t gx = std::max(1u, std::min(ntiles, 2 * cus / std::max(1u, mtiles * p.Z)));
+  const uint32_t gx = std::max(1u, std::min(ntiles, 4 * cus / std::max(1u, mtiles * p.Z)));
   if (mtiles > 65535u) return fail(STS_ERR_INVALID, "M = %u too large", p.M);
   const dim3 grid(gx, mtiles, p.Z), block(64 * KB);
-  if (p.swiglu_f)
-    hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, block, 0, stream, p);
+  if (KB <= 4) {
+    if (p.swiglu_f)
+      hipLaunchKernelGGL((q4k_gemm_kernel<true, 256>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((q4k_gemm_kernel<false, 256>), grid, block, 0, stream, p);
+  } else {
+    if (p.swiglu_f)
+      hipLaunchKernelGGL((q4k_gemm_kernel<true, 1024>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((q4k_gemm_kernel<false, 1024>), grid, block, 0, stream, p);
+  }
   STS_HIP(hipGetLastError());
   return STS_OK;
 }

@@ -3,10 +3,10 @@
 // sts_depformer_generate issues, on one stream, the launches of
 // DepthEngine::generate (crates/sts-wasm/src/depth_engine.rs:884-1491) for a
 // batch of streams: one GEMM for the input projections of every step, then
-// per step an embedding + add, per layer RMSNorm, QKV GEMM, fused
-// cache-write + attention, out_proj GEMM + residual, RMSNorm, linear_in GEMM
-// with SwiGLU, linear_out GEMM + residual, and finally the output GEMM and
-// the sampler.  Nothing is allocated or read back per call.
+// per step an embedding + add, per layer the QKV GEMM (RMSNorm fused on its
+// input), fused cache-write + attention, out_proj GEMM + residual, linear_in
+// GEMM (RMSNorm on its input, SwiGLU on its output), linear_out GEMM +
+// residual, and finally the output GEMM and the sampler.  Nothing is allocated or read back per call.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -39,9 +39,9 @@ struct sts_depformer {
 
 extern "C" {
 
-int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* residual,
-                 uint64_t ldr, float* y, uint64_t ldy, uint32_t rows, uint32_t k, uint32_t n,
-                 int swiglu, void* stream) {
+int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* norm_alpha,
+                 float norm_eps, const float* residual, uint64_t ldr, float* y, uint64_t ldy,
+                 uint32_t rows, uint32_t k, uint32_t n, int swiglu, void* stream) {
   sts::clear_error();
   STS_CHECK(weights && x && y, "null pointer argument");
   STS_CHECK(rows >= 1 && n >= 1, "empty shape");
@@ -49,6 +49,8 @@ int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const flo
             "row strides smaller than the rows");
   STS_CHECK(!swiglu || (n % 2 == 0 && !residual), "SwiGLU needs an even n and no residual");
   STS_CHECK(!residual || rows == 1 || ldr >= n, "residual stride smaller than n");
+  STS_CHECK(!norm_alpha || (aligned16(norm_alpha) && std::isfinite(norm_eps) && norm_eps >= 0.f),
+            "norm_alpha must be 16-byte aligned and norm_eps finite and >= 0");
   sts::Q4kGemmParams p;
   p.w[0] = weights;
   p.x = x;
@@ -61,6 +63,8 @@ int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const flo
   p.ldy = ldy;
   p.ldr = ldr;
   p.swiglu_f = swiglu ? n / 2 : 0;
+  p.norm_alpha = norm_alpha;
+  p.norm_eps = norm_eps;
   return sts::launch_q4k_gemm(p, as_stream(stream));
 }
 
@@ -223,8 +227,10 @@ int sts_depformer_generate(sts_depformer* d, const float* temporal_hidden,
   if (int rc = sts::launch_q4k_gemm(ip, st)) return rc;
 
   auto gemm = [&](const uint8_t* w, const float* x, uint32_t K, uint32_t N, const float* res,
-                  float* y, uint64_t ldy, uint32_t swiglu_f) {
+                  float* y, uint64_t ldy, uint32_t swiglu_f, const float* norm = nullptr) {
     sts::Q4kGemmParams p;
+    p.norm_alpha = norm;
+    p.norm_eps = c.rms_eps;
     p.w[0] = w;
     p.x = x;
     p.ldx = K;
@@ -258,9 +264,9 @@ int sts_depformer_generate(sts_depformer* d, const float* temporal_hidden,
       const size_t wi = (size_t)l * S + s;
       float* kl = d->kc + (size_t)l * B * H * M * hd;
       float* vl = d->vc + (size_t)l * B * H * M * hd;
-      if (int rc = sts::launch_rmsnorm(d->h, d->norm1[l], d->nrm, batch, D, c.rms_eps, st))
-        return rc;
-      if (int rc = gemm(d->attn_in_proj[wi], d->nrm, D, 3 * D, nullptr, d->qkv, 3 * D, 0))
+      // RMSNorm 1 fused into the QKV projection (:1069-1119).
+      if (int rc = gemm(d->attn_in_proj[wi], d->h, D, 3 * D, nullptr, d->qkv, 3 * D, 0,
+                        d->norm1[l]))
         return rc;
       // Cache write of K and V at slot s and attention over slots 0..s
       // (:1121-1209), one launch.
@@ -282,9 +288,9 @@ int sts_depformer_generate(sts_depformer* d, const float* temporal_hidden,
       a.scale_log2 = sts::softmax_scale_log2(c.attn_scale);
       if (int rc = sts::launch_decode(a, batch, hd, s + 1, st)) return rc;
       if (int rc = gemm(d->attn_out_proj[wi], d->att, D, D, d->h, d->h2, D, 0)) return rc;
-      if (int rc = sts::launch_rmsnorm(d->h2, d->norm2[l], d->nrm, batch, D, c.rms_eps, st))
+      // RMSNorm 2 fused into linear_in, SwiGLU into its output (:1262-1332).
+      if (int rc = gemm(d->ffn_in[wi], d->h2, D, 2 * F, nullptr, d->sw, F, F, d->norm2[l]))
         return rc;
-      if (int rc = gemm(d->ffn_in[wi], d->nrm, D, 2 * F, nullptr, d->sw, F, F)) return rc;
       if (int rc = gemm(d->ffn_out[wi], d->sw, F, D, d->h2, d->h, D, 0)) return rc;
     }
     float* lg = logits ? logits + (size_t)s * B * V : d->logits;

@@ -82,7 +82,8 @@ SIGNATURES = {
     "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
     "sts_q4k_matvec": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "sts_q4k_dequant": (_int, [_vp, _vp, _u32, _u32, _vp]),
-    "sts_q4k_gemm": (_int, [_vp, _vp, _u64, _vp, _u64, _vp, _u64, _u32, _u32, _u32, _int, _vp]),
+    "sts_q4k_gemm": (_int, [_vp, _vp, _u64, _vp, _f32, _vp, _u64, _vp, _u64, _u32, _u32, _u32,
+                            _int, _vp]),
     "sts_rmsnorm": (_int, [_vp, _vp, _vp, _u32, _u32, _f32, _vp]),
     "sts_embed_add_q4_0": (_int, [_vp, _u32, _vp, _u64, _vp, _vp, _u32, _u32, _vp]),
     "sts_sample_topk": (_int, [_vp, _u64, _u32, _u32, _u32, _f32, _f32, _vp, _vp, _u64, _vp,
@@ -500,8 +501,8 @@ def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch
         _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out), B, k,
                                      n, _stream(stream)))
     else:
-        _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, _ptr(res), n, _ptr(out), n,
-                                   B * Mrows, k, n, 0, _stream(stream)))
+        _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, None, 0.0, _ptr(res), n,
+                                   _ptr(out), n, B * Mrows, k, n, 0, _stream(stream)))
     return out
 
 
@@ -533,9 +534,12 @@ class Q4KLinear:
 # ---------------------------------------------------------------------------
 
 def q4k_gemm(x: torch.Tensor, weights: Q4KTensor, residual: Optional[torch.Tensor] = None,
-             swiglu: bool = False, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+             swiglu: bool = False, norm_alpha: Optional[torch.Tensor] = None,
+             norm_eps: float = 0.0, out: Optional[torch.Tensor] = None,
+             stream=None) -> torch.Tensor:
     """x [R, K] -> [R, N] = x @ W^T (+ residual); with swiglu, W has 2F rows and
-    the result is silu(G[:, :F]) * G[:, F:] ([R, F])."""
+    the result is silu(G[:, :F]) * G[:, F:] ([R, F]); with norm_alpha, x is
+    RMS-normalised first."""
     n, k = weights.shape()
     R = x.shape[0]
     x = x.reshape(R, k).contiguous()
@@ -543,8 +547,9 @@ def q4k_gemm(x: torch.Tensor, weights: Q4KTensor, residual: Optional[torch.Tenso
     if out is None:
         out = torch.empty((R, nout), dtype=torch.float32, device=x.device)
     res = residual.reshape(R, n).contiguous() if residual is not None else None
-    _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, _ptr(res), n, _ptr(out), nout,
-                               R, k, n, 1 if swiglu else 0, _stream(stream)))
+    _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, _ptr(norm_alpha), norm_eps,
+                               _ptr(res), n, _ptr(out), nout, R, k, n, 1 if swiglu else 0,
+                               _stream(stream)))
     return out
 
 

@@ -189,12 +189,14 @@ def test_counters_match_oracle_over_random_walk(M):
 def test_depformer_chain_argument_errors():
     """Rejected before any device work (no GPU needed)."""
     lib = sts_attn.load()
-    assert "multiple of 256" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1000, None, 0, FAKE, 3072, 64,
-                                                      1000, 3072, 0, None))
-    assert "SwiGLU" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, FAKE, 5632, FAKE, 2816, 64, 1024,
-                                             5632, 1, None))
-    assert "strides" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 512, None, 0, FAKE, 3072, 64, 1024,
-                                              3072, 0, None))
+    assert "multiple of 256" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1000, None, 0.0, None, 0, FAKE,
+                                                      3072, 64, 1000, 3072, 0, None))
+    assert "SwiGLU" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, None, 0.0, FAKE, 5632, FAKE, 2816,
+                                             64, 1024, 5632, 1, None))
+    assert "strides" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 512, None, 0.0, None, 0, FAKE, 3072, 64,
+                                              1024, 3072, 0, None))
+    assert "norm_eps" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, FAKE, -1.0, None, 0, FAKE, 3072,
+                                               64, 1024, 3072, 0, None))
     assert "null" in _err(lib.sts_rmsnorm(None, FAKE, FAKE, 4, 1024, 1e-8, None))
     assert "eps" in _err(lib.sts_rmsnorm(FAKE, FAKE, FAKE, 4, 1024, float("nan"), None))
     assert "multiple of 32" in _err(lib.sts_embed_add_q4_0(FAKE, 10, FAKE, 1, FAKE, FAKE, 2, 100,

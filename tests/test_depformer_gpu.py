@@ -83,6 +83,33 @@ def test_q4k_gemm_against_oracle(gpu, M, N, K, res):
     assert (np.abs(got - refw) <= 2 * tol).all()
 
 
+@pytest.mark.parametrize("M,N,K,swiglu", [(64, 3072, 1024, False), (5, 5632, 1024, True),
+                                          (3, 1024, 4096, False)])
+def test_q4k_gemm_fused_rmsnorm(gpu, M, N, K, swiglu):
+    """RMSNorm on the GEMM's input: against the shader-order RMSNorm followed
+    by the f64 product (the normalised x differ in the last ulp at most)."""
+    blocks = oracle.q4k_random_blocks(M * 3 + N + K, N, K)
+    x = oracle.normal(M + 5, (M, K)) * np.float32(3.0)
+    alpha = (1 + 0.1 * oracle.normal(K, (K,))).astype(np.float32)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    got = host(sts_attn.q4k_gemm(dev(x), w, swiglu=swiglu, norm_alpha=dev(alpha),
+                                 norm_eps=1e-8)).astype(np.float64)
+    xn = oracle.rmsnorm_wgsl(x, alpha, 1e-8)
+    y = oracle.q4k_matvec_f64(blocks, xn, N)
+    b = 1e-5 * q4k_bound(blocks, xn, N)
+    if swiglu:
+        F = N // 2
+        g, v = y[:, :F], y[:, F:]
+        sig = 1 / (1 + np.exp(-g))
+        want = g * sig * v
+        # + 1e-30: silu underflows to 0 in f32 where g is very negative.
+        tol = (np.abs(sig * (1 + g * (1 - sig))) * np.abs(v) * b[:, :F] + np.abs(g * sig) * b[:, F:]
+               + 1e-6 * np.abs(want) + 1e-30)
+    else:
+        want, tol = y, b
+    assert (np.abs(got - want) <= tol).all(), (np.abs(got - want) / tol).max()
+
+
 def test_q4k_gemm_swiglu(gpu):
     M, F, K = 64, 2816, 1024
     blocks = oracle.q4k_random_blocks(31, 2 * F, K)
