@@ -88,16 +88,58 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
   // x values of this lane: X[m][256 kb + 64 g + j], j < 64 (zero past M).
   const uint32_t m = mt * 16 + r;
   const bool m_ok = m < p.M;
-  const float4* xr =
-      reinterpret_cast<const float4*>(X + (size_t)(m_ok ? m : 0) * p.ldx + 256 * kb + 64 * g);
   float xv[64];
+  if constexpr (MAXT <= 256) {
+    // Through a per-wave LDS chunk (16 rows x 64 floats, pitch 68) so the
+    // global loads are coalesced: instruction i of chunk c reads rows
+    // 4i..4i+3, 256 contiguous bytes each; the lanes of slot g then copy
+    // chunk g (the 16 lanes of a read phase hit distinct banks).
+    __shared__ __align__(16) float xs[MAXT / 64][16][68];
+    float4 ld[4][4];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float4 t = xr[j];
-    xv[4 * j] = m_ok ? t.x : 0.f;
-    xv[4 * j + 1] = m_ok ? t.y : 0.f;
-    xv[4 * j + 2] = m_ok ? t.z : 0.f;
-    xv[4 * j + 3] = m_ok ? t.w : 0.f;
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t mm = mt * 16 + 4 * i + (lane >> 4);
+        const float4 t = *(reinterpret_cast<const float4*>(
+                               X + (size_t)(mm < p.M ? mm : 0) * p.ldx + 256 * kb + 64 * c) +
+                           (lane & 15));
+        ld[c][i] = mm < p.M ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(&xs[kb][4 * i + (lane >> 4)][4 * (lane & 15)]) = ld[c][i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (g == c) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float4 t = *reinterpret_cast<const float4*>(&xs[kb][r][4 * j]);
+          xv[4 * j] = t.x;
+          xv[4 * j + 1] = t.y;
+          xv[4 * j + 2] = t.z;
+          xv[4 * j + 3] = t.w;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  } else {
+    // Wide workgroups (K > 1024) read their rows directly.
+    const float4* xr =
+        reinterpret_cast<const float4*>(X + (size_t)(m_ok ? m : 0) * p.ldx + 256 * kb + 64 * g);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float4 t = xr[j];
+      xv[4 * j] = m_ok ? t.x : 0.f;
+      xv[4 * j + 1] = m_ok ? t.y : 0.f;
+      xv[4 * j + 2] = m_ok ? t.z : 0.f;
+      xv[4 * j + 3] = m_ok ? t.w : 0.f;
+    }
   }
   if (p.norm_alpha) {
     // RMSNorm of the 16 rows (shader_rmsnorm.wgsl:80-90): x * (1/rms) * alpha,

@@ -121,14 +121,23 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
   uint32_t base = blockIdx.x * (G * U);
   load(ra, base);
 
-  // This lane's 64 x values, kept in registers for the whole launch (read
-  // from L2: every wave of the grid reads x once).
-  const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
+  // This lane's 64 x values, kept in registers for the whole launch.  The
+  // workgroup reads x once with coalesced loads into LDS, slot c at row c of
+  // pitch 68 floats (the 16 lanes of a read phase then hit distinct banks),
+  // and each lane copies its slot.
+  extern __shared__ __align__(16) float xs[];  // [K/64][68]
+  {
+    const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
+    const uint32_t n4 = p.K / 4;
+    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x)
+      *reinterpret_cast<float4*>(&xs[(i >> 4) * 68 + 4 * (i & 15)]) = xb[i];
+    __syncthreads();
+  }
   float xv[64];
-  const uint32_t xs0 = has ? s * 16 : 0u;
+  const uint32_t xs0 = has ? s * 68 : 0u;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float4 t = xb[xs0 + j];
+    const float4 t = *reinterpret_cast<const float4*>(&xs[xs0 + 4 * j]);
     xv[4 * j] = has ? t.x : 0.f;
     xv[4 * j + 1] = has ? t.y : 0.f;
     xv[4 * j + 2] = has ? t.z : 0.f;
@@ -228,17 +237,20 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
   }
 }
 
+constexpr uint32_t kWavesPerCu = 4;
+
 template <int KP>
 int launch_kp(const Q4kParams& p, hipStream_t stream) {
   constexpr int G = KP == 1 ? 4 : (KP == 2 ? 2 : 1);
   constexpr int U = 2;
-  // About one workgroup (four waves) per CU walking the rows: more waves
-  // only add reads of x and launch work (measured), fewer leave CUs idle.
+  // kWavesPerCu waves per CU walking the rows; each workgroup reads x once
+  // into LDS.
   const uint32_t cus = (uint32_t)device_cu_count();
   const uint32_t steps = (p.N + G * U - 1) / (G * U);
-  const uint32_t wgs = std::max(1u, std::min(steps, cus * 4 / (KP * G)));
-  hipLaunchKernelGGL((q4k_matvec_kernel<KP, G, U>), dim3(wgs, p.B), dim3(64 * KP * G), 0, stream,
-                     p);
+  const uint32_t wgs = std::max(1u, std::min(steps, cus * kWavesPerCu / (KP * G)));
+  const size_t lds = (size_t)(p.K / 64) * 68 * sizeof(float);
+  hipLaunchKernelGGL((q4k_matvec_kernel<KP, G, U>), dim3(wgs, p.B), dim3(64 * KP * G), lds,
+                     stream, p);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }
