@@ -166,7 +166,9 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
   }
 
   for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    load_w(nxt, t + gridDim.x);  // next tile in flight during this one
+    // The next tile's weights are in flight during this one (the condition
+    // is uniform over the workgroup).
+    if (t + gridDim.x < ntiles) load_w(nxt, t + gridDim.x);
 #pragma unroll
     for (int hv = 0; hv < NH; ++hv) {
       const u32x4 hd = cur[hv].hd, qa = cur[hv].qa, qb = cur[hv].qb;
