@@ -7,7 +7,9 @@ Inputs are regenerated at test time from the SplitMix64/Box-Muller spec
 (oracle.normal); each fixture stores the seeds, shapes, the SHA-256 of the
 generated inputs (so a changed generator is caught) and the expected outputs:
 `out_wgsl` (the shader's own f32 order) and `out_f64` (closed form in double).
-Q4_K cases also store their weight blocks and the dequantised weights.
+Q4_K cases also store their weight blocks and the dequantised weights; the
+depformer chain case stores its tokens, per-step logits and sampling inputs
+(its weights are regenerated from a seed and checked by hash).
 RoPE (theta 1e4, interleaved) is applied to Q and K at their logical
 positions, as the configs specify.
 """
@@ -66,6 +68,33 @@ def q4k_case(seed, N, K, B, quantized=False):
                 out_f64=oracle.q4k_matvec_f64(blocks, x, N))
 
 
+DEPF_CFG = dict(num_steps=4, num_layers=2, dim=256, num_heads=4, ffn=512, temporal_dim=512,
+                out_vocab=128, text_emb_vocab=300, audio_emb_vocab=129, num_audio_emb=3,
+                kv_max_len=5, rms_eps=1e-8, attn_scale=0.125)
+
+
+def depformer_case(seed, wseed):
+    """The depformer step chain on one stream at a small shape: weights from
+    oracle.DepformerWeights.synthetic(seed=wseed) (hashed, not stored), the
+    temporal hidden state from oracle.normal(seed), top_k 20, temperature
+    0.8, penalty 1.2.  out_wgsl: the oracle's logits per step; out_f64: the
+    float64 restatement of the chain fed the same tokens."""
+    from test_oracle_depformer import _chain_f64
+    w = oracle.DepformerWeights.synthetic(DEPF_CFG, seed=wseed)
+    S = DEPF_CFG["num_steps"]
+    th = oracle.normal(seed, (DEPF_CFG["temporal_dim"],))
+    rand = np.array([0.31, 0.77, 0.05, 0.52], np.float32)
+    pt = np.zeros((S, 30), np.uint32)
+    pt[1, :4] = [3, 9, 3, 200]
+    npn = np.array([0, 4, 0, 0], np.uint32)
+    tokens, logits, _ = oracle.depformer_generate(w, th, 17, 20, 0.8, 1.2, rand, pt, npn)
+    weights = [a for f in oracle.DepformerWeights.FIELDS for a in getattr(w, f)] + [w.text_emb]
+    return dict(seed=seed, wseed=wseed, text_token=17, top_k=20, temperature=0.8, penalty=1.2,
+                rand=rand, penalty_tokens=pt, num_penalty=npn,
+                input_sha=sha(th, *weights), tokens=tokens, out_wgsl=logits,
+                out_f64=_chain_f64(w, th, 17, tokens))
+
+
 CASES = {
     # BASELINE config 1: 1 layer, 32 x 128, L = 256, window at slot 0.
     "decode_config1": lambda: decode_case(101, 32, 128, 256, 256, 0),
@@ -83,6 +112,8 @@ CASES = {
     # and quantizer-made blocks.
     "q4k_random": lambda: q4k_case(909, 6, 768, 2),
     "q4k_quantized": lambda: q4k_case(1010, 4, 512, 1, quantized=True),
+    # The depformer step chain (depth_engine.rs:884-1491), one stream, small shape.
+    "depformer_chain_small": lambda: depformer_case(1111, 3),
 }
 
 

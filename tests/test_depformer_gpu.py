@@ -224,6 +224,50 @@ def test_depformer_chain_small(gpu):
     eng.close()
 
 
+def test_depformer_chain_golden_fixture(gpu):
+    """tests/golden/depformer_chain_small.npz: the GPU chain's tokens equal
+    the fixture's and its logits are within 1e-4 of their scale."""
+    import os
+    from conftest import GOLDEN
+    f = np.load(os.path.join(GOLDEN, "depformer_chain_small.npz"))
+    w = oracle.DepformerWeights.synthetic(CFG, seed=int(f["wseed"]))
+    th = oracle.normal(int(f["seed"]), (CFG["temporal_dim"],))[None]
+    text = np.array([int(f["text_token"])], np.uint32)
+    eng = sts_attn.DepthEngine(_config(CFG), _device_weights(w), max_batch=1)
+    logits = torch.empty((CFG["num_steps"], 1, CFG["out_vocab"]), device="cuda")
+    tok = eng.generate(dev(th), dev(text.view(np.int32)), float(f["temperature"]),
+                       int(f["top_k"]), float(f["penalty"]), dev(f["rand"][None]),
+                       dev(f["penalty_tokens"][None].view(np.int32)),
+                       dev(f["num_penalty"][None].view(np.int32)), logits=logits)
+    np.testing.assert_array_equal(host(tok).view(np.uint32)[0], f["tokens"])
+    lg = host(logits)[:, 0]
+    assert np.abs(lg - f["out_wgsl"]).max() <= 1e-4 * np.abs(f["out_wgsl"]).max()
+    assert np.abs(lg - f["out_f64"]).max() <= 1e-4 * np.abs(f["out_f64"]).max()
+    eng.close()
+
+
+@pytest.mark.parametrize("top_k", [0, 200])
+def test_depformer_chain_edge_cases(gpu, top_k):
+    """3 steps with one audio table (steps 1 and 2 both read it), an
+    out-of-vocab text token (zero embedding), penalty tokens past the vocab,
+    greedy (top_k = 0) and top_k above the vocab; batch 2 of max 3."""
+    cfg = dict(CFG, num_steps=3, num_audio_emb=1, kv_max_len=3)
+    w = oracle.DepformerWeights.synthetic(cfg, seed=9)
+    B = 2
+    th, text, rand, pt, npn = _inputs(cfg, B, 5)
+    text[0] = cfg["text_emb_vocab"] + 7
+    pt[:, :, :4] = cfg["out_vocab"] + np.arange(4, dtype=np.uint32)
+    npn[:] = 30
+    eng = sts_attn.DepthEngine(_config(cfg), _device_weights(w), max_batch=3)
+    logits = torch.empty((3, B, cfg["out_vocab"]), device="cuda")
+    tok = eng.generate(dev(th), dev(text.view(np.int32)), 0.7, top_k, 0.9, dev(rand),
+                       dev(pt.view(np.int32)), dev(npn.view(np.int32)), logits=logits)
+    n = _check_streams(cfg, w, th, text, rand, pt, npn, host(tok).view(np.uint32), host(logits),
+                       top_k, 0.7, 0.9, range(B))
+    assert n >= B * 3 - 1
+    eng.close()
+
+
 @pytest.fixture(scope="module")
 def full_model():
     cfg = {f: getattr(sts_attn.DepformerConfig.personaplex(), f)
