@@ -377,8 +377,9 @@ typedef struct sts_depformer_config {
  * attn_out_proj, ffn_linear_in, ffn_linear_out indexed [layer*num_steps + step],
  * shapes [3 dim][dim], [dim][dim], [2 ffn][dim], [dim][ffn];
  * output_linear[step] [out_vocab][dim].  f32 alphas per layer.  Q4_0 tables
- * text_emb [text_emb_vocab][dim], audio_emb[i] [audio_emb_vocab][dim].  The
- * pointer arrays themselves are host memory and are copied at create.
+ * text_emb [text_emb_vocab][dim], audio_emb[i] [audio_emb_vocab][dim].  Every
+ * pointer must be 16-byte aligned.  The pointer arrays themselves are host
+ * memory and are copied at create.
  */
 typedef struct sts_depformer_weights {
   const uint8_t* const* input_proj;

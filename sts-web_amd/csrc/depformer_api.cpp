@@ -158,7 +158,7 @@ int sts_depformer_create(const sts_depformer_config* cfg, const sts_depformer_we
                   &d->ffn_in, &d->ffn_out, &d->audio_emb})
     for (const uint8_t* p : *v) ok = ok && p && aligned16(p);
   for (auto* v : {&d->norm1, &d->norm2})
-    for (const float* p : *v) ok = ok && p;
+    for (const float* p : *v) ok = ok && p && aligned16(p);
   if (!ok) {
     delete d;
     return sts::fail(STS_ERR_INVALID, "weight pointers must be non-null and 16-byte aligned");
