@@ -422,12 +422,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   if (lane == 0) atomicExch(ctr, 0u);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  if (!s || !*s) return dflt;
-  return atoi(s);
-}
-
 }  // namespace
 
 int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
@@ -447,10 +441,10 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
     if (chunk == 0) chunk = kRpi;
     nsplit = 1;
   } else {
-    static const int target_mult = env_int("STS_DECODE_WG_PER_CU", 1);
-    static const int chunk_max = env_int("STS_DECODE_CHUNK_MAX", 512);
-    static const int chunk_min = env_int("STS_DECODE_CHUNK_MIN", 64);
-    const uint64_t target = (uint64_t)device_cu_count() * (uint64_t)target_mult;
+    // One workgroup per CU (2-4 per CU measured slower: more partials to
+    // merge, no more bytes in flight per CU).
+    constexpr int chunk_max = 512, chunk_min = 64;
+    const uint64_t target = (uint64_t)device_cu_count();
     uint64_t want = (target + units - 1) / units;
     if (want < 1) want = 1;
     uint64_t c = (max_rows + want - 1) / want;
@@ -468,7 +462,6 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   }
   p.chunk = chunk;
   p.nsplit_max = nsplit;
-  static const bool pipe = env_int("STS_DECODE_PIPE", 1) != 0;
   if (nsplit > 1) {
     // Partials and arrival counters.
     Workspace* ws = nullptr;
@@ -483,17 +476,13 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   if (head_dim == 128) {
     if (waves == 1)
       hipLaunchKernelGGL((decode_kernel<128, 1, false>), grid, dim3(64), 0, stream, p);
-    else if (pipe)
-      hipLaunchKernelGGL((decode_kernel<128, 4, true>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<128, 4, false>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 4, true>), grid, dim3(256), 0, stream, p);
   } else if (head_dim == 64) {
     if (waves == 1)
       hipLaunchKernelGGL((decode_kernel<64, 1, false>), grid, dim3(64), 0, stream, p);
-    else if (pipe)
-      hipLaunchKernelGGL((decode_kernel<64, 4, true>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<64, 4, false>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, 4, true>), grid, dim3(256), 0, stream, p);
   } else {
     return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
   }

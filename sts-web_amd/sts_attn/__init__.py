@@ -7,6 +7,8 @@ This module mirrors the reference's Rust interface for the path
     gpu_cache_write_v(v, cache, offset, max_len)  model.rs:143-188
     KVCache / LayerCaches                          model.rs:195-411
     RoPE                                           model.rs:38-122
+    Q4KTensor / q4k_matmul / Q4KLinear             gguf.rs:520-905
+    DepthEngine.generate                           depth_engine.rs:884-1491
 
 over the C ABI declared in include/sts_attn.h.  Device memory comes from
 torch tensors (float32, on a ROCm device); every call goes through the HIP
