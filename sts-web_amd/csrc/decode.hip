@@ -38,11 +38,7 @@ __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<floa
 
 // K/V rows are read once per launch: nontemporal (streaming) loads keep them
 // from displacing useful lines and measure ~9% faster on this access pattern.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 ld4_stream(const float* p) {
-  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-  return make_float4(v.x, v.y, v.z, v.w);
-}
+constexpr int kNt = 2;  // buffer-load cache policy bit: nontemporal
 
 // Interleaved RoPE of two adjacent pairs (model.rs:99-100), each product and
 // sum rounded separately as the reference evaluates them.
@@ -109,7 +105,7 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-template <int D, int WAVES, bool PIPE>
+template <int D, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p) {
   constexpr int G = D / 4;
   constexpr int NG = 64 / G;
@@ -169,45 +165,55 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   q4.w *= p.scale_log2;
 
   const size_t kvoff = b * p.kv_bstride + h * p.kv_hstride;
-  const float* kh = p.k + kvoff + c * 4;
-  const float* vh = p.v + kvoff + c * 4;
+  // K/V rows come in through buffer loads on per-(stream, head) resources:
+  // a row outside the window gets an offset past the resource and loads
+  // zeros, so every load is issued unconditionally and the compiler's wait
+  // counts see one fixed order of loads (no drain before each batch).
+  const uint32_t head_bytes = p.M * (uint32_t)(D * sizeof(float));
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.k) + kvoff, 0, (int)head_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.v) + kvoff, 0, (int)head_bytes, kBufferWord3);
   const bool append = p.k_new != nullptr;
   const uint32_t new_row = len - 1;
+  const uint32_t new_unit = new_row / RPI;
+  const int new_g = (int)((new_row % RPI) % NG), new_j = (int)((new_row % RPI) / NG);
+
+  // The fused-append row: RoPE'd in registers, written to its slot once (by
+  // the wave whose unit holds it) and used from registers by that wave.
+  float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
+  if (append) {
+    kn = ld4(p.k_new + qoff);
+    vn = ld4(p.v_new + qoff);
+  }
 
   float m = -FLT_MAX;
   float lsum = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   const int jj = (c >> 2) & (RPG - 1);
 
-  // Loads rows r0 + j*NG + g (j < RPG) of this lane's group into kk/vv; the
-  // fused-append row is taken from k_new/v_new and written to its slot.
+  // Loads rows r0 + j*NG + g (j < RPG) of this lane's group into kk/vv.
   auto load_rows = [&](uint32_t r0, float4* kk, float4* vv) {
 #pragma unroll
     for (int j = 0; j < RPG; ++j) {
       const uint32_t r = r0 + j * NG + g;
       uint32_t slot = start + r;
       slot = slot >= p.M ? slot - p.M : slot;
-      if (r < len) {
-        if (append && r == new_row) {
-          float4 kn = ld4(p.k_new + qoff);
-          const float4 vn = ld4(p.v_new + qoff);
-          if (rope) kn = rope4(kn, rc, rs);
-          st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
-          st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
-          kk[j] = kn;
-          vv[j] = vn;
-        } else {
-          kk[j] = ld4_stream(kh + (size_t)slot * D);
-          vv[j] = ld4_stream(vh + (size_t)slot * D);
-        }
-      } else {
-        kk[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        vv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      const uint32_t off = r < len ? slot * (uint32_t)(D * sizeof(float)) + c * 16 : 0x80000000u;
+      kk[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, kNt));
+      vv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, kNt));
     }
   };
   // Online-softmax update with the 16 rows starting at r0.
-  auto consume_rows = [&](uint32_t r0, const float4* kk, const float4* vv) {
+  auto consume_rows = [&](uint32_t r0, float4* kk, float4* vv) {
+    if (append && r0 == new_unit * RPI && g == new_g) {
+#pragma unroll
+      for (int j = 0; j < RPG; ++j)
+        if (j == new_j) {
+          kk[j] = kn;
+          vv[j] = vn;
+        }
+    }
     float s[RPG];
 #pragma unroll
     for (int j = 0; j < RPG; ++j)
@@ -246,29 +252,36 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     }
   };
 
+  // Writes the fused-append row to its slot (RoPE'd first).  The one-wave
+  // kernel (short windows) issues its first loads before this store; the
+  // 4-wave kernel stores first (measured: 19.1 vs 20.3 us per config-2 launch
+  // the other way round; 3.93 vs 4.03 us per depformer step).
+  auto store_new_row = [&]() {
+    if (!append) return;
+    if (rope) kn = rope4(kn, rc, rs);
+    const uint32_t owner_split = new_unit % nsplit;
+    const uint32_t owner_wave = (new_unit / nsplit) % WAVES;
+    if (split == owner_split && (uint32_t)wave == owner_wave && g == new_g) {
+      uint32_t slot = start + new_row;
+      slot = slot >= p.M ? slot - p.M : slot;
+      st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
+      st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
+    }
+  };
+  // One batch of 16 rows in flight per wave (16 KB, 64 KB per CU): loads,
+  // then the online-softmax update.  Deeper register pipelines (2-4 batches)
+  // lowered the HBM rate through the extra outstanding requests (config 2:
+  // 19.4 us per launch with one batch, 20.4-21.1 us with 2-4).
   const uint32_t ustep = nsplit * WAVES;
   uint32_t u = split + nsplit * wave;
-  if constexpr (PIPE) {
-    // Two register buffers: the next 16 rows are in flight while the current
-    // 16 are consumed, so each wave always has a full batch of loads queued.
-    float4 ka[RPG], va[RPG], kb[RPG], vb[RPG];
-    if (u < nunits) load_rows(u * RPI, ka, va);
-    while (u < nunits) {
-      const uint32_t u1 = u + ustep;
-      if (u1 < nunits) load_rows(u1 * RPI, kb, vb);
-      consume_rows(u * RPI, ka, va);
-      if (u1 >= nunits) break;
-      const uint32_t u2 = u1 + ustep;
-      if (u2 < nunits) load_rows(u2 * RPI, ka, va);
-      consume_rows(u1 * RPI, kb, vb);
-      u = u2;
-    }
-  } else {
-    for (; u < nunits; u += ustep) {
-      float4 kk[RPG], vv[RPG];
-      load_rows(u * RPI, kk, vv);
-      consume_rows(u * RPI, kk, vv);
-    }
+  float4 kk[RPG], vv[RPG];
+  if constexpr (WAVES > 1) store_new_row();
+  if (u < nunits) load_rows(u * RPI, kk, vv);
+  if constexpr (WAVES == 1) store_new_row();
+  while (u < nunits) {
+    consume_rows(u * RPI, kk, vv);
+    u += ustep;
+    if (u < nunits) load_rows(u * RPI, kk, vv);
   }
 
   // Merge the NG row groups of the wave (lanes c, c+G, ... hold the same dims).
@@ -470,19 +483,21 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
     p.part = ws->part;
     p.counters = ws->counters;
   }
+  if ((uint64_t)p.M * head_dim * sizeof(float) > 0x7FFFFFF0ull)
+    return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
   if (batch > 65535u || p.H > 65535u)
     return fail(STS_ERR_INVALID, "batch (%u) and heads (%u) must be <= 65535", batch, p.H);
   const dim3 grid(nsplit, p.H, batch);
   if (head_dim == 128) {
     if (waves == 1)
-      hipLaunchKernelGGL((decode_kernel<128, 1, false>), grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 1>), grid, dim3(64), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<128, 4, true>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 4>), grid, dim3(256), 0, stream, p);
   } else if (head_dim == 64) {
     if (waves == 1)
-      hipLaunchKernelGGL((decode_kernel<64, 1, false>), grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, 1>), grid, dim3(64), 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<64, 4, true>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, 4>), grid, dim3(256), 0, stream, p);
   } else {
     return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
   }
