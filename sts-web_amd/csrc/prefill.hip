@@ -4,30 +4,28 @@
 // softmax((Q K^T) * scale + mask) V with key j masked when j > offset + i
 // (apply_causal_mask, model.rs:539-563), here over a ring window that may wrap.
 //
-// One workgroup = one head x 64 queries; keys stream through LDS in blocks of
-// 64.  Eight waves: wave w owns queries 16*(w%4)..+15 and key slice w/4 (32
-// keys) of every block, with its own online softmax; the two slices of a
-// query group merge through LDS at the end.  Each wave computes S^T = K Q^T,
-// so that the accumulator layout of S^T (lane l: keys 4*(l/16)+j of each
-// 16-key tile, query l%16) is, after the online softmax, directly the B
-// operand P^T of O^T = V^T P^T.  The contraction order over keys is permuted
-// identically in V^T and P^T, so P never goes through LDS.  Each query's max
-// and sum are reduced over the 4 lanes {l%16 + 16g} that hold its keys.
+// Two kernels, one workgroup = one head x 64 queries, keys in blocks of 64:
 //
-//   BF16 = true : f32 K/V/Q rounded to bf16 while staging, v_mfma_f32_16x16x32_bf16,
-//                 f32 softmax and accumulation.
-//   BF16 = false: f32 throughout, v_mfma_f32_16x16x4f32.
+//   prefill_kernel (f32, v_mfma_f32_16x16x4f32): eight waves; wave w owns
+//   queries 16*(w%4)..+15 and key slice w/4 (32 keys) of every block, with
+//   its own online softmax; the two slices of a query group merge through
+//   LDS at the end.  Each wave computes S^T = K Q^T, so that the accumulator
+//   layout of S^T (lane l: keys 4*(l/16)+j of each 16-key tile, query l%16)
+//   is, after the online softmax, directly the B operand P^T of
+//   O^T = V^T P^T; the contraction order over keys is permuted identically
+//   in V^T and P^T, so P never goes through LDS.  Each tile's key range is
+//   also split over up to four workgroups (blockIdx.z); each publishes
+//   (O, max, sum) with device-coherent stores and the last to arrive folds
+//   them in split order.
 //
-// The f32 variant also splits each tile's key range over up to four
-// workgroups (blockIdx.z); each publishes (O, max, sum) with device-coherent
-// stores and the last to arrive folds them in split order.
+//   prefill_ws_kernel (bf16 MFMA, f32 softmax and accumulation): specialised
+//   producer and consumer waves, described above the kernel.
 //
-// Blocks are indexed (head, q-tile, split) with head fastest, so all
+// Blocks are indexed (head, q-tile[, split]) with head fastest, so all
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
 // L2 copy of the head's K/V; the heaviest (last) q-tiles are dispatched first.
 #include <algorithm>
 #include <cfloat>
-#include <type_traits>
 
 #include "coherent.hpp"
 #include "common.hpp"
@@ -41,7 +39,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;  // queries per workgroup
 constexpr int kBK = 64;  // keys per LDS block
@@ -52,13 +49,12 @@ __device__ __forceinline__ float4 scale4(float4 x, float c) {
   return make_float4(x.x * c, x.y * c, x.z * c, x.w * c);
 }
 
-template <int D, bool BF16>
+template <int D>
 struct PrefillSmem {
-  using T = typename std::conditional<BF16, __bf16, float>::type;
-  static constexpr int KP = BF16 ? D + 8 : D + 4;  // K row pitch: 16 rows hit distinct banks
-  static constexpr int VP = 80;                    // V^T row pitch (keys), see vt_col
-  alignas(16) T ks[kBK * KP];
-  alignas(16) T vt[D * VP];
+  static constexpr int KP = D + 4;  // K row pitch: 16 rows hit distinct banks
+  static constexpr int VP = 80;     // V^T row pitch (keys), see vt_col
+  alignas(16) float ks[kBK * KP];
+  alignas(16) float vt[D * VP];
 };
 
 constexpr int kMaxPrefillSplits = 4;
@@ -76,10 +72,10 @@ __device__ __forceinline__ int vt_col(int d, int quad) {
 // 16 * (w % 4) .. +15 of the tile and the key slice w / 4 (32 keys) of every
 // 64-key block, with its own online softmax; the slices merge once at the
 // end.  More waves per SIMD hide the latency of each wave's serial
-// softmax/MFMA chain.
-template <int D, bool BF16, int KSPLIT>
+// softmax/MFMA chain.  f32 throughout.
+template <int D, int KSPLIT>
 __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillParams p) {
-  using Smem = PrefillSmem<D, BF16>;
+  using Smem = PrefillSmem<D>;
   constexpr int NT = 256 * KSPLIT;
   constexpr int KP = Smem::KP;
   constexpr int VP = Smem::VP;
@@ -91,11 +87,8 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   constexpr int VSQ = (kBK / 4) * C4;  // V 4-key x 4-dim squares per block
   constexpr int VPER = VSQ >= NT ? VSQ / NT : 1;
   static_assert(KPER >= 1 && TW == 2, "tile shape: 32-key slices");
-  // bf16 tiles are double-buffered (block i+1 is staged while block i is
-  // computed, one barrier per block); f32 tiles are twice as large and use one
-  // buffer with a barrier on each side of the staging.
-  constexpr int NBUF = BF16 ? 2 : 1;
-  __shared__ Smem sm_buf[NBUF];
+  // One LDS buffer, with a barrier on each side of the staging.
+  __shared__ Smem sm_buf[1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -118,27 +111,17 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   const uint32_t w_wave = base_w + min(p.S - 1, qt * kBQ + qg * 16 + 15);
 
   // B operand of S^T = K Q^T: this lane's query row, permuted per MFMA.
-  constexpr int QN = BF16 ? D / 32 : D / 16;
-  typename std::conditional<BF16, bf16x8, float4>::type qop[QN];
+  constexpr int QN = D / 16;
+  float4 qop[QN];
+  // Every lane loads (a row past the tile's end reads row 0) and scales by
+  // zero when it has no query: no branch, so all loads issue at once.
   const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
+  const float qs = q_ok ? p.scale_log2 : 0.f;
 #pragma unroll
   for (int a = 0; a < QN; ++a) {
-    if constexpr (BF16) {
-      // dims 32a + 8g .. +7
-      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-      if (q_ok) {
-        x0 = scale4(ld4(qrow + a * 32 + g * 8), p.scale_log2);
-        x1 = scale4(ld4(qrow + a * 32 + g * 8 + 4), p.scale_log2);
-      }
-      bf16x8 b;
-      b[0] = (__bf16)x0.x; b[1] = (__bf16)x0.y; b[2] = (__bf16)x0.z; b[3] = (__bf16)x0.w;
-      b[4] = (__bf16)x1.x; b[5] = (__bf16)x1.y; b[6] = (__bf16)x1.z; b[7] = (__bf16)x1.w;
-      qop[a] = b;
-    } else {
-      // dims 16a + 4g .. +3 (instruction (a, j) contracts dim 16a + 4g + j)
-      qop[a] = q_ok ? scale4(ld4(qrow + a * 16 + g * 4), p.scale_log2)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    // dims 16a + 4g .. +3 (instruction (a, j) contracts dim 16a + 4g + j)
+    qop[a] = scale4(ld4(qrow + a * 16 + g * 4), qs);
+  
   }
 
   float m = -FLT_MAX;
@@ -228,13 +211,8 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
     for (int i = 0; i < KPER; ++i) {
       const int key = tid / C4 + i * (NT / C4);
       const floatx4 x = b.k[i];
-      if constexpr (BF16) {
-        bf16x4 y;
-        y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
-        *reinterpret_cast<bf16x4*>(&sm.ks[key * KP + d4 * 4]) = y;
-      } else {
-        *reinterpret_cast<floatx4*>(&sm.ks[key * KP + d4 * 4]) = x;
-      }
+      *reinterpret_cast<floatx4*>(&sm.ks[key * KP + d4 * 4]) = x;
+    
     }
     if (v_thread) {
 #pragma unroll
@@ -248,14 +226,9 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
           const float e1 = c == 0 ? x[1].x : c == 1 ? x[1].y : c == 2 ? x[1].z : x[1].w;
           const float e2 = c == 0 ? x[2].x : c == 1 ? x[2].y : c == 2 ? x[2].z : x[2].w;
           const float e3 = c == 0 ? x[3].x : c == 1 ? x[3].y : c == 2 ? x[3].z : x[3].w;
-          if constexpr (BF16) {
-            bf16x4 y;
-            y[0] = (__bf16)e0; y[1] = (__bf16)e1; y[2] = (__bf16)e2; y[3] = (__bf16)e3;
-            *reinterpret_cast<bf16x4*>(&sm.vt[d * VP + vt_col(d, kq)]) = y;
-          } else {
-            *reinterpret_cast<float4*>(&sm.vt[d * VP + vt_col(d, kq)]) =
-                make_float4(e0, e1, e2, e3);
-          }
+          *reinterpret_cast<float4*>(&sm.vt[d * VP + vt_col(d, kq)]) =
+              make_float4(e0, e1, e2, e3);
+        
         }
       }
     }
@@ -269,52 +242,28 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
     if (!active || k0 > w_wave) return;    // every key of the slice is masked for this wave
     const bool unmasked = k0 + KW <= kend && k0 + KW - 1 <= w_first;
 
-    // S^T tiles t: keys k0 + 16t + 4g + j, query qi.  The bf16 operands of
+    // S^T tiles t: keys k0 + 16t + 4g + j, query qi.  The operands of
     // the whole block (K for S^T, V^T for O^T) are read from LDS first, so
     // the reads overlap each other, the MFMAs and the softmax.
     const int q0 = kslice * (KW / 4);  // first 4-key quad of the slice
     floatx4 s[TW];
-    [[maybe_unused]] bf16x8 vop[DT];
-    if constexpr (BF16) {
-      bf16x8 kop[TW][QN];
 #pragma unroll
-      for (int t = 0; t < TW; ++t)
+    for (int t = 0; t < TW; ++t) {
+      const int krow = kslice * KW + 16 * t + l16;
+      float4 kf[QN];
 #pragma unroll
-        for (int a = 0; a < QN; ++a)
-          kop[t][a] = *reinterpret_cast<const bf16x8*>(
-              &sm.ks[(kslice * KW + 16 * t + l16) * KP + a * 32 + g * 8]);
+      for (int a = 0; a < QN; ++a)
+        kf[a] = *reinterpret_cast<const float4*>(&sm.ks[krow * KP + a * 16 + g * 4]);
+      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const int d = 16 * t + l16;
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + g)]);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&sm.vt[d * VP + vt_col(d, q0 + 4 + g)]);
-        vop[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int t = 0; t < TW; ++t) {
-        s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int a = 0; a < QN; ++a)
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[t][a], qop[a], s[t], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < TW; ++t) {
-        const int krow = kslice * KW + 16 * t + l16;
-        float4 kf[QN];
-#pragma unroll
-        for (int a = 0; a < QN; ++a)
-          kf[a] = *reinterpret_cast<const float4*>(&sm.ks[krow * KP + a * 16 + g * 4]);
-        s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int a = 0; a < QN; ++a) {
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].x, qop[a].x, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].y, qop[a].y, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].z, qop[a].z, s[t], 0, 0, 0);
-          s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].w, qop[a].w, s[t], 0, 0, 0);
-        }
+      for (int a = 0; a < QN; ++a) {
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].x, qop[a].x, s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].y, qop[a].y, s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].z, qop[a].z, s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[a].w, qop[a].w, s[t], 0, 0, 0);
       }
     }
+  
 
     // Causal mask and online softmax for query qi over this slice (q carries
     // the scale, so scores are already in log2 units).
@@ -357,59 +306,31 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
     }
 
     // O^T += V^T P^T over this wave's 32 keys.
-    if constexpr (BF16) {
-      bf16x8 pb;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pb[j] = (__bf16)s[0][j];
-        pb[4 + j] = (__bf16)s[1][j];
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int tk = 0; tk < TW; ++tk) {
+        const int d = 16 * t + l16;
+        const float4 vf =
+            *reinterpret_cast<const float4*>(&sm.vt[d * VP + vt_col(d, q0 + 4 * tk + g)]);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[tk][0], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[tk][1], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[tk][2], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, s[tk][3], o[t], 0, 0, 0);
       }
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[t], pb, o[t], 0, 0, 0);
-    } else {
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int tk = 0; tk < TW; ++tk) {
-          const int d = 16 * t + l16;
-          const float4 vf =
-              *reinterpret_cast<const float4*>(&sm.vt[d * VP + vt_col(d, q0 + 4 * tk + g)]);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, s[tk][0], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, s[tk][1], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, s[tk][2], o[t], 0, 0, 0);
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, s[tk][3], o[t], 0, 0, 0);
-        }
-    }
+  
   };
 
   // One block in flight in registers while the previous one computes.
   auto blk = [&](uint32_t i) { return kb_begin + min(i, nblk - 1) * kBK; };
-  if constexpr (NBUF == 2) {
-    // While block i is computed from one LDS buffer, block i+1 (in registers
-    // since the previous trip) is staged into the other and block i+2 is
-    // fetched.  The other buffer was last read by block i-1, which every wave
-    // finished before the previous barrier.
-    fetch(buf, blk(0), true);
+  fetch(buf, kb_begin, true);
+  for (uint32_t i = 0; i < nblk; ++i) {
+    const uint32_t kb = kb_begin + i * kBK;
+    __syncthreads();  // the previous block's LDS reads are done
     stage(buf, 0);
-    fetch(buf, blk(1), nblk > 1);
     __syncthreads();
-    for (uint32_t i = 0; i < nblk; ++i) {
-      compute(blk(i), i & 1, true);
-      if (i + 1 < nblk) stage(buf, (i + 1) & 1);
-      fetch(buf, blk(i + 2), i + 2 < nblk);
-      __syncthreads();
-    }
-  } else {
-    fetch(buf, kb_begin, true);
-    for (uint32_t i = 0; i < nblk; ++i) {
-      const uint32_t kb = kb_begin + i * kBK;
-      __syncthreads();  // the previous block's LDS reads are done
-      stage(buf, 0);
-      __syncthreads();
-      fetch(buf, blk(i + 1), i + 1 < nblk);
-      compute(kb, 0, true);
-    }
+    fetch(buf, blk(i + 1), i + 1 < nblk);
+    compute(kb, 0, true);
   }
 
   // Merge the key slices of each query group: slice r > 0 parks (m, l, O^T)
@@ -548,18 +469,367 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   if (tid == 0) atomicExch(ctr, 0u);
 }
 
-template <int D, bool BF16>
-int launch_t(const PrefillParams& p, hipStream_t stream) {
+// ---------------------------------------------------------------------------
+// bf16 prefill with specialised waves.
+//
+// One workgroup = one head x 64 queries, eight waves.  Waves 4..7 (producers)
+// load the f32 K/V rows of 64-key blocks, two blocks in flight in registers,
+// round them to bf16 and write them into a ring of kWsStages LDS stages (K
+// row-major, V transposed).  Waves 0..3 (consumers) each own 32 queries
+// (w & 1) and one 32-key slice (w >> 1) of every block; per block a consumer
+// computes S^T = K_slice Q^T as one 32x32 tile (v_mfma_f32_32x32x16_bf16,
+// Q^T in registers), the online softmax, and O^T += V^T P^T with the S^T
+// accumulator itself as the B operand (lane l: query l%32, register v: key
+// 8*(v/4) + 4*(l/32) + v%4 of the slice; V^T holds the keys of every 16-key
+// group in the order bit 3 <-> bit 2 so the A operand reads them in the same
+// order).  Producers and consumers of a stage hand over through two LDS
+// counters per stage (filled: +1 per producer wave, released: +1 per
+// consumer wave), so loading and converting overlap the matrix and softmax
+// work instead of alternating with it at workgroup barriers.
+constexpr int kWsStages = 4;
+constexpr int kWsKB = 64;
+
+template <int D>
+struct WsStage {
+  static constexpr int KP = D + 8;      // K row pitch (bf16)
+  static constexpr int VP = kWsKB + 8;  // V^T row pitch (bf16)
+  alignas(16) __bf16 ks[kWsKB * KP];
+  alignas(16) __bf16 vt[D * VP];
+};
+
+// bf16 offset of block key k (0..63) inside V^T row d: key bits 2 and 3
+// swapped, then 8-key units XOR-permuted by (d/4)%8 (bank spread for the
+// transposing writes and the operand reads).
+__device__ __forceinline__ int ws_vt_pos(int d, int k) {
+  const int kp = (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+  return (((kp >> 3) ^ ((d >> 2) & 7)) << 3) | (kp & 7);
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// Spins until the LDS counter reaches target.  The handover is expected to
+// complete within microseconds; the bound only guarantees that every wave
+// leaves the loop.
+__device__ __forceinline__ void ws_wait_ge(const uint32_t* ctr, uint32_t target) {
+  for (uint32_t spin = 0; spin < (1u << 24); ++spin) {
+    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+}
+// Publishes this wave's LDS writes (or the end of its LDS reads) and counts it.
+__device__ __forceinline__ void ws_signal(uint32_t* ctr, int lane) {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  if (lane == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) {
+  using Stage = WsStage<D>;
+  constexpr int KB = kWsKB;
+  constexpr int NS = kWsStages;
+  constexpr int QT = 64;
+  constexpr int KP = Stage::KP;
+  constexpr int VP = Stage::VP;
+  constexpr int C4 = D / 4;               // float4 columns of a row
+  constexpr int KA = D / 16;              // k-chunks of S^T
+  constexpr int OT = D / 32;              // O^T row tiles
+  constexpr int NP = 256;                 // producer threads
+  constexpr int KPER = KB * C4 / NP;      // K float4 per producer thread per block
+  constexpr int VSQ = (KB / 4) * C4;      // V 4-key x 4-dim squares per block
+  constexpr int VPER = VSQ >= NP ? VSQ / NP : 1;
+  static_assert(KPER >= 1 && (VSQ % NP == 0 || NP % VSQ == 0), "tile shape");
+  __shared__ Stage st[NS];
+  __shared__ uint32_t filled[NS], released[NS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t h = blockIdx.x;
+  const uint32_t nqt = (p.S + QT - 1) / QT;
+  const uint32_t qt = nqt - 1 - blockIdx.y;  // heaviest tiles first
+  const uint32_t base_w = p.len - p.S;
+  const uint32_t q_last = min(p.S, (qt + 1) * QT) - 1;
+  const uint32_t kend = min(p.len, base_w + q_last + 1);
+  const uint32_t nblk = (kend + KB - 1) / KB;
+  if (tid < NS) {
+    filled[tid] = 0;
+    released[tid] = 0;
+  }
+  __syncthreads();
+
+  // Consumer state (also the merge's inputs).
+  const int qg = wave & 1;
+  const int ks = (wave >> 1) & 1;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const uint32_t qi = qt * QT + qg * 32 + l32;
+  const bool q_ok = qi < p.S;
+  float m = -FLT_MAX;
+  float lsum = 0.f;
+  f32x16 o[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
+
+  if (wave >= 4) {
+    // ---- producers ----
+    const int pt = tid - 256;
+    const int d4 = pt % C4;
+    constexpr uint32_t ROWB = D * sizeof(float);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.k) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.v) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+    const bool v_thread = VSQ >= NP || pt < VSQ;
+    auto k_row = [&](int i) { return (uint32_t)(pt / C4 + i * (NP / C4)); };
+    auto v_row = [&](int i, int r4) { return (uint32_t)((pt / C4 + i * (NP / C4)) * 4 + r4); };
+    struct Buf {
+      floatx4 k[KPER];
+      floatx4 v[VPER][4];
+    };
+    constexpr int NL = KPER + 4 * VPER;
+    // Loads block b (rows past the tile's last key, and every row of a block
+    // past the last, read zeros: the loads are issued unconditionally so the
+    // compiler's wait counts see one fixed order).
+    auto fetch = [&](Buf& bf, uint32_t b) {
+      const uint32_t kb = b * KB;
+      const uint32_t lim = b < nblk ? kend : 0u;
+      uint32_t slot0 = p.start + kb;
+      slot0 = slot0 >= p.M ? slot0 - p.M : slot0;
+      uint32_t vo[NL];
+      uint32_t so = 0;
+      if (kb + KB <= lim && slot0 + KB <= p.M) {
+        so = slot0 * ROWB;
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) vo[i] = k_row(i) * ROWB + d4 * 16;
+#pragma unroll
+        for (int i = 0; i < VPER; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) vo[KPER + 4 * i + r4] = v_row(i, r4) * ROWB + d4 * 16;
+      } else {
+        auto off = [&](uint32_t r) {
+          const uint32_t row = kb + r;
+          uint32_t slot = slot0 + r;
+          slot = min(slot, slot - p.M);  // wrap (slot < 2M)
+          return row < lim ? slot * ROWB + d4 * 16 : 0xFFFFFFF0u;
+        };
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) vo[i] = off(k_row(i));
+#pragma unroll
+        for (int i = 0; i < VPER; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) vo[KPER + 4 * i + r4] = off(v_row(i, r4));
+      }
+#pragma unroll
+      for (int i = 0; i < KPER; ++i)
+        bf.k[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo[i], so, 0));
+      if (v_thread) {
+#pragma unroll
+        for (int i = 0; i < VPER; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            bf.v[i][r4] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo[KPER + 4 * i + r4], so, 0));
+      }
+    };
+    auto put = [&](const Buf& bf, Stage& sg) {
+#pragma unroll
+      for (int i = 0; i < KPER; ++i) {
+        const floatx4 x = bf.k[i];
+        bf16x4 y;
+        y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
+        *reinterpret_cast<bf16x4*>(&sg.ks[k_row(i) * KP + d4 * 4]) = y;
+      }
+      if (!v_thread) return;
+#pragma unroll
+      for (int i = 0; i < VPER; ++i) {
+        const int key0 = (pt / C4 + i * (NP / C4)) * 4;
+        const floatx4* x = bf.v[i];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int d = d4 * 4 + c;
+          bf16x4 y;
+          y[0] = (__bf16)x[0][c]; y[1] = (__bf16)x[1][c]; y[2] = (__bf16)x[2][c]; y[3] = (__bf16)x[3][c];
+          *reinterpret_cast<bf16x4*>(&sg.vt[d * VP + ws_vt_pos(d, key0)]) = y;
+        }
+      }
+    };
+    // Block i goes to stage i % NS once the consumers have released that
+    // stage's previous block (4 releases per use).
+    auto produce = [&](const Buf& bf, uint32_t i) {
+      const uint32_t s = i % NS, use = i / NS;
+      ws_wait_ge(&released[s], 4 * use);
+      put(bf, st[s]);
+      ws_signal(&filled[s], lane);
+    };
+    // Block 0 alone first (it is what every consumer waits for), then two
+    // blocks in flight in registers.
+    Buf ba, bb;
+    fetch(ba, 0);
+    produce(ba, 0);
+    fetch(ba, 1);
+    for (uint32_t i = 1; i < nblk; i += 2) {
+      fetch(bb, i + 1);
+      produce(ba, i);
+      if (i + 1 >= nblk) break;
+      fetch(ba, i + 2);
+      produce(bb, i + 1);
+    }
+  } else {
+    // ---- consumers ----
+    const uint32_t w_q = base_w + qi;
+    const uint32_t w_first = base_w + qt * QT + qg * 32;
+    bf16x8 qop[KA];
+    {
+      // Every lane loads (a row past the tile's end reads row 0) and scales
+      // by zero when it has no query: no branch, so all loads issue at once.
+      const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
+      const float qs = q_ok ? p.scale_log2 : 0.f;
+#pragma unroll
+      for (int a = 0; a < KA; ++a) {
+        const float4 x0 = scale4(ld4(qrow + a * 16 + hh * 8), qs);
+        const float4 x1 = scale4(ld4(qrow + a * 16 + hh * 8 + 4), qs);
+        bf16x8 b;
+        b[0] = (__bf16)x0.x; b[1] = (__bf16)x0.y; b[2] = (__bf16)x0.z; b[3] = (__bf16)x0.w;
+        b[4] = (__bf16)x1.x; b[5] = (__bf16)x1.y; b[6] = (__bf16)x1.z; b[7] = (__bf16)x1.w;
+        qop[a] = b;
+      }
+    }
+    for (uint32_t i = 0; i < nblk; ++i) {
+      const uint32_t s = i % NS, use = i / NS;
+      ws_wait_ge(&filled[s], 4 * (use + 1));
+      const Stage& sg = st[s];
+      const uint32_t k0 = i * KB + ks * 32;
+      bf16x8 kop[KA];
+#pragma unroll
+      for (int a = 0; a < KA; ++a)
+        kop[a] = *reinterpret_cast<const bf16x8*>(&sg.ks[(ks * 32 + l32) * KP + a * 16 + hh * 8]);
+      bf16x8 vop[OT][2];
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int d = 32 * t + l32;
+          const int oct = (ks * 4 + 2 * c + hh) ^ ((d >> 2) & 7);
+          vop[t][c] = *reinterpret_cast<const bf16x8*>(&sg.vt[d * VP + oct * 8]);
+        }
+      f32x16 sc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+#pragma unroll
+      for (int a = 0; a < KA; ++a)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[a], sc, 0, 0, 0);
+      // The operands are in registers: the stage can be refilled.
+      ws_signal(&released[s], lane);
+
+      const bool unmasked = k0 + 31 < kend && k0 + 31 <= w_first;
+      float mx = -INFINITY;
+      if (unmasked) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[v]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t key = k0 + 8 * (v >> 2) + 4 * hh + (v & 3);
+          const float x = (key <= w_q && key < kend) ? sc[v] : -INFINITY;
+          sc[v] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = max_xor32(mx);
+      const float mn = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float e = fast_exp2(sc[v] - mn);
+        sc[v] = e;
+        ps += e;
+      }
+      ps = sum_xor32(ps);
+      lsum = lsum * alpha + ps;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int t = 0; t < OT; ++t) o[t] *= alpha;
+      }
+      bf16x8 pb[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)sc[8 * c + j];
+#pragma unroll
+      for (int t = 0; t < OT; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[t][c], pb[c], o[t], 0, 0, 0);
+    }
+  }
+
+  // Merge the two key slices of each query group through LDS (stage 0, free
+  // once every wave has passed the barrier) and write the rows.
+  __syncthreads();
+  constexpr int RS = OT * 16 + 2;
+  float* red = reinterpret_cast<float*>(&st[0]);  // [2 groups][64 lanes][RS]
+  static_assert(2 * 64 * RS * sizeof(float) <= sizeof(Stage), "merge scratch");
+  if (wave < 4 && ks == 1) {
+    float* dst = red + (qg * 64 + lane) * RS;
+#pragma unroll
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dst[16 * t + v] = o[t][v];
+    dst[OT * 16] = m;
+    dst[OT * 16 + 1] = lsum;
+  }
+  __syncthreads();
+  if (wave >= 4 || ks != 0 || !q_ok) return;
+  const float* src = red + (qg * 64 + lane) * RS;
+  const float m2 = src[OT * 16], l2 = src[OT * 16 + 1];
+  const float mm = fmaxf(m, m2);
+  const float f1 = fast_exp2(m - mm), f2 = fast_exp2(m2 - mm);
+  const float inv = 1.f / (lsum * f1 + l2 * f2);
+  float* orow = p.out + ((size_t)qi * p.H + h) * D;
+#pragma unroll
+  for (int t = 0; t < OT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float4 y;
+      y.x = (o[t][4 * r + 0] * f1 + src[16 * t + 4 * r + 0] * f2) * inv;
+      y.y = (o[t][4 * r + 1] * f1 + src[16 * t + 4 * r + 1] * f2) * inv;
+      y.z = (o[t][4 * r + 2] * f1 + src[16 * t + 4 * r + 2] * f2) * inv;
+      y.w = (o[t][4 * r + 3] * f1 + src[16 * t + 4 * r + 3] * f2) * inv;
+      *reinterpret_cast<float4*>(orow + 32 * t + 8 * r + 4 * hh) = y;
+    }
+}
+
+template <int D>
+int launch_ws(const PrefillParams& p, hipStream_t stream) {
+  const uint32_t nqt = (p.S + 63) / 64;
+  if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
+  if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
+    return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
+  hipLaunchKernelGGL((prefill_ws_kernel<D>), dim3(p.H, nqt, 1), dim3(512), 0, stream, p);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+template <int D>
+int launch_f32(const PrefillParams& p, hipStream_t stream) {
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
   if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
   // f32 tiles carry four times the MFMA work of bf16 ones: split their key
-  // ranges until there are about two workgroups per CU.  bf16 tiles are
-  // bound by the CU's load rate and gain nothing from splitting.
+  // ranges until there are about two workgroups per CU.
   const uint32_t tiles = p.H * nqt;
   const uint32_t cus = (uint32_t)device_cu_count();
-  uint32_t nsplit = BF16 ? 1u : (2 * cus + tiles - 1) / tiles;
+  uint32_t nsplit = (2 * cus + tiles - 1) / tiles;
   nsplit = std::max(1u, std::min<uint32_t>(nsplit, kMaxPrefillSplits));
   PrefillParams q = p;
   q.nsplit = nsplit;
@@ -570,7 +840,7 @@ int launch_t(const PrefillParams& p, hipStream_t stream) {
     q.part = ws->part;
     q.counters = ws->counters;
   }
-  hipLaunchKernelGGL((prefill_kernel<D, BF16, kKsplit>), dim3(p.H, nqt, nsplit),
+  hipLaunchKernelGGL((prefill_kernel<D, kKsplit>), dim3(p.H, nqt, nsplit),
                      dim3(256 * kKsplit), 0, stream, q);
   STS_HIP(hipGetLastError());
   return STS_OK;
@@ -580,8 +850,8 @@ int launch_t(const PrefillParams& p, hipStream_t stream) {
 
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream) {
   const bool bf16 = precision == STS_PREC_BF16_MFMA;
-  if (head_dim == 128) return bf16 ? launch_t<128, true>(p, stream) : launch_t<128, false>(p, stream);
-  if (head_dim == 64) return bf16 ? launch_t<64, true>(p, stream) : launch_t<64, false>(p, stream);
+  if (head_dim == 128) return bf16 ? launch_ws<128>(p, stream) : launch_f32<128>(p, stream);
+  if (head_dim == 64) return bf16 ? launch_ws<64>(p, stream) : launch_f32<64>(p, stream);
   return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
 }
 
