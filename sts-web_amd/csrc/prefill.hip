@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
 // bf16 prefill with specialised waves.
 //
 // One workgroup = one head x 64 queries, eight waves.  Waves 4..7 (producers)
-// load the f32 K/V rows of 64-key blocks, two blocks in flight in registers,
+// load the f32 K/V rows of 64-key blocks, three blocks in flight in registers,
 // round them to bf16 and write them into a ring of kWsStages LDS stages (K
 // row-major, V transposed).  Waves 0..3 (consumers) each own 32 queries
 // (w & 1) and one 32-key slice (w >> 1) of every block; per block a consumer
@@ -668,18 +668,22 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       put(bf, st[s]);
       ws_signal(&filled[s], lane);
     };
-    // Block 0 alone first (it is what every consumer waits for), then two
-    // blocks in flight in registers.
-    Buf ba, bb;
-    fetch(ba, 0);
-    produce(ba, 0);
-    fetch(ba, 1);
-    for (uint32_t i = 1; i < nblk; i += 2) {
-      fetch(bb, i + 1);
-      produce(ba, i);
+    // Three blocks in flight in registers: block i is converted and stored
+    // while blocks i+1 and i+2 load (the per-CU load rate, not the issue,
+    // bounds this loop).
+    Buf b0, b1, b2;
+    fetch(b0, 0);
+    fetch(b1, 1);
+    produce(b0, 0);
+    for (uint32_t i = 1; i < nblk; i += 3) {
+      fetch(b2, i + 1);
+      produce(b1, i);
       if (i + 1 >= nblk) break;
-      fetch(ba, i + 2);
-      produce(bb, i + 1);
+      fetch(b0, i + 2);
+      produce(b2, i + 1);
+      if (i + 2 >= nblk) break;
+      fetch(b1, i + 3);
+      produce(b0, i + 2);
     }
   } else {
     // ---- consumers ----
@@ -706,27 +710,18 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       ws_wait_ge(&filled[s], 4 * (use + 1));
       const Stage& sg = st[s];
       const uint32_t k0 = i * KB + ks * 32;
-      bf16x8 kop[KA];
-#pragma unroll
-      for (int a = 0; a < KA; ++a)
-        kop[a] = *reinterpret_cast<const bf16x8*>(&sg.ks[(ks * 32 + l32) * KP + a * 16 + hh * 8]);
-      bf16x8 vop[OT][2];
-#pragma unroll
-      for (int t = 0; t < OT; ++t)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int d = 32 * t + l32;
-          const int oct = (ks * 4 + 2 * c + hh) ^ ((d >> 2) & 7);
-          vop[t][c] = *reinterpret_cast<const bf16x8*>(&sg.vt[d * VP + oct * 8]);
-        }
       f32x16 sc;
+      {
+        bf16x8 kop[KA];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+        for (int a = 0; a < KA; ++a)
+          kop[a] = *reinterpret_cast<const bf16x8*>(&sg.ks[(ks * 32 + l32) * KP + a * 16 + hh * 8]);
 #pragma unroll
-      for (int a = 0; a < KA; ++a)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[a], sc, 0, 0, 0);
-      // The operands are in registers: the stage can be refilled.
-      ws_signal(&released[s], lane);
+        for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+#pragma unroll
+        for (int a = 0; a < KA; ++a)
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[a], sc, 0, 0, 0);
+      }
 
       const bool unmasked = k0 + 31 < kend && k0 + 31 <= w_first;
       float mx = -INFINITY;
@@ -764,11 +759,22 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)sc[8 * c + j];
+      // V^T operands are read per output tile after the softmax (the stage
+      // stays claimed until they are in registers), then the stage is released.
 #pragma unroll
-      for (int t = 0; t < OT; ++t)
+      for (int t = 0; t < OT; ++t) {
+        bf16x8 vop[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int d = 32 * t + l32;
+          const int oct = (ks * 4 + 2 * c + hh) ^ ((d >> 2) & 7);
+          vop[c] = *reinterpret_cast<const bf16x8*>(&sg.vt[d * VP + oct * 8]);
+        }
 #pragma unroll
         for (int c = 0; c < 2; ++c)
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[t][c], pb[c], o[t], 0, 0, 0);
+          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[c], pb[c], o[t], 0, 0, 0);
+      }
+      ws_signal(&released[s], lane);
     }
   }
 
