@@ -544,7 +544,11 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   constexpr int VPER = VSQ >= NP ? VSQ / NP : 1;
   static_assert(KPER >= 1 && (VSQ % NP == 0 || NP % VSQ == 0), "tile shape");
   __shared__ Stage st[NS];
-  __shared__ uint32_t filled[NS], released[NS];
+  __shared__ uint32_t filled[NS], released[NS], q_ready;
+  // The tile's queries, scaled and rounded to bf16 once by the producers
+  // (each query row is the B operand of two consumer waves).
+  constexpr int QP = D + 8;  // row pitch (bf16)
+  __shared__ __align__(16) __bf16 qs[QT * QP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -559,6 +563,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   if (tid < NS) {
     filled[tid] = 0;
     released[tid] = 0;
+    if (tid == 0) q_ready = 0;
   }
   __syncthreads();
 
@@ -671,9 +676,27 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // Three blocks in flight in registers: block i is converted and stored
     // while blocks i+1 and i+2 load (the per-CU load rate, not the issue,
     // bounds this loop).
+    // Queries first: row pt/C4 + i*(NP/C4), columns 4*d4..+3 (a row past the
+    // tile's end reads row 0 and is scaled by zero, so every load is issued).
+    constexpr int QPER = QT * C4 / NP;
+    float4 qv[QPER];
+#pragma unroll
+    for (int i = 0; i < QPER; ++i) {
+      const uint32_t qq = qt * QT + k_row(i);
+      qv[i] = ld4(p.q + ((size_t)(qq < p.S ? qq : 0) * p.H + h) * D + d4 * 4);
+    }
     Buf b0, b1, b2;
     fetch(b0, 0);
     fetch(b1, 1);
+#pragma unroll
+    for (int i = 0; i < QPER; ++i) {
+      const uint32_t qq = qt * QT + k_row(i);
+      const float4 x = scale4(qv[i], qq < p.S ? p.scale_log2 : 0.f);
+      bf16x4 y;
+      y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
+      *reinterpret_cast<bf16x4*>(&qs[k_row(i) * QP + d4 * 4]) = y;
+    }
+    ws_signal(&q_ready, lane);
     produce(b0, 0);
     for (uint32_t i = 1; i < nblk; i += 3) {
       fetch(b2, i + 1);
@@ -690,21 +713,10 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     const uint32_t w_q = base_w + qi;
     const uint32_t w_first = base_w + qt * QT + qg * 32;
     bf16x8 qop[KA];
-    {
-      // Every lane loads (a row past the tile's end reads row 0) and scales
-      // by zero when it has no query: no branch, so all loads issue at once.
-      const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
-      const float qs = q_ok ? p.scale_log2 : 0.f;
+    ws_wait_ge(&q_ready, 4);
 #pragma unroll
-      for (int a = 0; a < KA; ++a) {
-        const float4 x0 = scale4(ld4(qrow + a * 16 + hh * 8), qs);
-        const float4 x1 = scale4(ld4(qrow + a * 16 + hh * 8 + 4), qs);
-        bf16x8 b;
-        b[0] = (__bf16)x0.x; b[1] = (__bf16)x0.y; b[2] = (__bf16)x0.z; b[3] = (__bf16)x0.w;
-        b[4] = (__bf16)x1.x; b[5] = (__bf16)x1.y; b[6] = (__bf16)x1.z; b[7] = (__bf16)x1.w;
-        qop[a] = b;
-      }
-    }
+    for (int a = 0; a < KA; ++a)
+      qop[a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
     for (uint32_t i = 0; i < nblk; ++i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&filled[s], 4 * (use + 1));
