@@ -473,7 +473,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
-              f"(the path shards by head or stream; see DESIGN.md)", file=sys.stderr)
+              f"(the attention path would shard by head or by stream, one GPU each; "
+              f"this build runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
     import torch
     import sts_attn as sts
