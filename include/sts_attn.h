@@ -57,8 +57,13 @@ enum sts_status {
 };
 
 enum sts_precision {
-  STS_PREC_F32 = 0,      /* f32 inputs, f32 arithmetic                       */
-  STS_PREC_BF16_MFMA = 1 /* f32 inputs rounded to bf16 for MFMA, f32 accumulate */
+  STS_PREC_F32 = 0,           /* f32 inputs, f32 arithmetic                  */
+  STS_PREC_BF16_MFMA = 1,     /* f32 inputs rounded to bf16 for MFMA, f32 accumulate */
+  STS_PREC_F32_SPLIT_BF16 = 2 /* f32 inputs split into bf16 hi + lo (16 significant
+                                 bits), each product as three bf16 MFMAs
+                                 (hi*hi + hi*lo + lo*hi), f32 accumulate: f32-level
+                                 results (within 1e-4 of f64 like STS_PREC_F32) on
+                                 the bf16 matrix rate.  Prefill only.            */
 };
 
 /* Message for the calling thread's most recent failed call ("" if none). */
@@ -145,7 +150,7 @@ int sts_depformer_step(const float* q, const float* k_new, const float* v_new,
  * (stream.rs:482-492).
  *   q, out     [seq][heads][head_dim]
  *   k/v cache  [heads][max_len][head_dim];  window row r in slot (win_start + r) % max_len
- * precision: STS_PREC_F32 or STS_PREC_BF16_MFMA.
+ * precision: STS_PREC_F32, STS_PREC_BF16_MFMA or STS_PREC_F32_SPLIT_BF16.
  */
 int sts_prefill_attention(const float* q, const float* k_cache, const float* v_cache,
                           float* out, uint32_t seq, uint32_t heads, uint32_t head_dim,

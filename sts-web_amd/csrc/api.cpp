@@ -214,7 +214,8 @@ int sts_prefill_attention(const float* q, const float* k_cache, const float* v_c
   STS_CHECK(seq >= 1 && seq <= win_len, "need 1 <= seq (%u) <= win_len (%u)", seq, win_len);
   STS_CHECK(win_len <= max_len, "win_len %u > max_len %u", win_len, max_len);
   STS_CHECK(win_start < max_len, "win_start %u >= max_len %u", win_start, max_len);
-  STS_CHECK(precision == STS_PREC_F32 || precision == STS_PREC_BF16_MFMA,
+  STS_CHECK(precision == STS_PREC_F32 || precision == STS_PREC_BF16_MFMA ||
+                precision == STS_PREC_F32_SPLIT_BF16,
             "precision %d unknown", precision);
   STS_CHECK(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
             "pointers must be 16-byte aligned");

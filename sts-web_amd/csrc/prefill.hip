@@ -489,13 +489,20 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
 constexpr int kWsStages = 4;
 constexpr int kWsKB = 64;
 
-template <int D>
+// SPLIT stages hold two bf16 planes of every value, x_hi = bf16(x) and
+// x_lo = bf16(x - x_hi) (16 significant bits between them).
+template <int D, bool SPLIT>
 struct WsStage {
   static constexpr int KP = D + 8;      // K row pitch (bf16)
   static constexpr int VP = kWsKB + 8;  // V^T row pitch (bf16)
-  alignas(16) __bf16 ks[kWsKB * KP];
-  alignas(16) __bf16 vt[D * VP];
+  static constexpr int NPL = SPLIT ? 2 : 1;
+  alignas(16) __bf16 ks[NPL][kWsKB * KP];
+  alignas(16) __bf16 vt[NPL][D * VP];
 };
+
+// x = hi + lo to 16 significant bits: hi = bf16(x), lo = bf16(x - hi) (the
+// difference is exact in f32).
+__device__ __forceinline__ __bf16 bf16_lo(float x, __bf16 hi) { return (__bf16)(x - (float)hi); }
 
 // bf16 offset of block key k (0..63) inside V^T row d: key bits 2 and 3
 // swapped, then 8-key units XOR-permuted by (d/4)%8 (bank spread for the
@@ -527,11 +534,17 @@ __device__ __forceinline__ void ws_signal(uint32_t* ctr, int lane) {
   if (lane == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <int D>
+// SPLIT: the f32-accurate variant.  Every operand is split into bf16 hi and
+// lo planes and each product runs as three bf16 MFMAs (hi*hi + hi*lo +
+// lo*hi, f32 accumulate; the dropped lo*lo term is 2^-16 relative), which
+// on this chip's 16:1 bf16:f32 matrix rate is ~5x the f32 MFMA rate.  Two
+// stages (the planes double a stage) and no LDS query tile: the consumers
+// split their own queries.
+template <int D, bool SPLIT>
 __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) {
-  using Stage = WsStage<D>;
+  using Stage = WsStage<D, SPLIT>;
   constexpr int KB = kWsKB;
-  constexpr int NS = kWsStages;
+  constexpr int NS = SPLIT ? 2 : kWsStages;
   constexpr int QT = 64;
   constexpr int KP = Stage::KP;
   constexpr int VP = Stage::VP;
@@ -548,7 +561,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   // The tile's queries, scaled and rounded to bf16 once by the producers
   // (each query row is the B operand of two consumer waves).
   constexpr int QP = D + 8;  // row pitch (bf16)
-  __shared__ __align__(16) __bf16 qs[QT * QP];
+  __shared__ __align__(16) __bf16 qs[SPLIT ? 8 : QT * QP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -643,13 +656,27 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
                 floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo[KPER + 4 * i + r4], so, 0));
       }
     };
+    // Four values rounded to bf16 at one offset of the hi plane (and, for
+    // SPLIT, their remainders in the lo plane).
+    auto store4 = [&](__bf16* hi_plane, __bf16* lo_plane, int off, float a, float b, float c, float d) {
+      bf16x4 yh, yl;
+      if constexpr (SPLIT) {
+        yh[0] = (__bf16)a; yh[1] = (__bf16)b; yh[2] = (__bf16)c; yh[3] = (__bf16)d;
+        yl[0] = bf16_lo(a, yh[0]); yl[1] = bf16_lo(b, yh[1]);
+        yl[2] = bf16_lo(c, yh[2]); yl[3] = bf16_lo(d, yh[3]);
+        *reinterpret_cast<bf16x4*>(&lo_plane[off]) = yl;
+      } else {
+        (void)lo_plane;
+        (void)yl;
+        yh[0] = (__bf16)a; yh[1] = (__bf16)b; yh[2] = (__bf16)c; yh[3] = (__bf16)d;
+      }
+      *reinterpret_cast<bf16x4*>(&hi_plane[off]) = yh;
+    };
     auto put = [&](const Buf& bf, Stage& sg) {
 #pragma unroll
       for (int i = 0; i < KPER; ++i) {
         const floatx4 x = bf.k[i];
-        bf16x4 y;
-        y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
-        *reinterpret_cast<bf16x4*>(&sg.ks[k_row(i) * KP + d4 * 4]) = y;
+        store4(sg.ks[0], sg.ks[Stage::NPL - 1], k_row(i) * KP + d4 * 4, x.x, x.y, x.z, x.w);
       }
       if (!v_thread) return;
 #pragma unroll
@@ -659,9 +686,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int d = d4 * 4 + c;
-          bf16x4 y;
-          y[0] = (__bf16)x[0][c]; y[1] = (__bf16)x[1][c]; y[2] = (__bf16)x[2][c]; y[3] = (__bf16)x[3][c];
-          *reinterpret_cast<bf16x4*>(&sg.vt[d * VP + ws_vt_pos(d, key0)]) = y;
+          store4(sg.vt[0], sg.vt[Stage::NPL - 1], d * VP + ws_vt_pos(d, key0), x[0][c], x[1][c], x[2][c], x[3][c]);
         }
       }
     };
@@ -678,25 +703,29 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // bounds this loop).
     // Queries first: row pt/C4 + i*(NP/C4), columns 4*d4..+3 (a row past the
     // tile's end reads row 0 and is scaled by zero, so every load is issued).
-    constexpr int QPER = QT * C4 / NP;
+    constexpr int QPER = SPLIT ? 1 : QT * C4 / NP;
     float4 qv[QPER];
+    if constexpr (!SPLIT) {
 #pragma unroll
-    for (int i = 0; i < QPER; ++i) {
-      const uint32_t qq = qt * QT + k_row(i);
-      qv[i] = ld4(p.q + ((size_t)(qq < p.S ? qq : 0) * p.H + h) * D + d4 * 4);
+      for (int i = 0; i < QPER; ++i) {
+        const uint32_t qq = qt * QT + k_row(i);
+        qv[i] = ld4(p.q + ((size_t)(qq < p.S ? qq : 0) * p.H + h) * D + d4 * 4);
+      }
     }
     Buf b0, b1, b2;
     fetch(b0, 0);
     fetch(b1, 1);
+    if constexpr (!SPLIT) {
 #pragma unroll
-    for (int i = 0; i < QPER; ++i) {
-      const uint32_t qq = qt * QT + k_row(i);
-      const float4 x = scale4(qv[i], qq < p.S ? p.scale_log2 : 0.f);
-      bf16x4 y;
-      y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
-      *reinterpret_cast<bf16x4*>(&qs[k_row(i) * QP + d4 * 4]) = y;
+      for (int i = 0; i < QPER; ++i) {
+        const uint32_t qq = qt * QT + k_row(i);
+        const float4 x = scale4(qv[i], qq < p.S ? p.scale_log2 : 0.f);
+        bf16x4 y;
+        y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
+        *reinterpret_cast<bf16x4*>(&qs[k_row(i) * QP + d4 * 4]) = y;
+      }
+      ws_signal(&q_ready, lane);
     }
-    ws_signal(&q_ready, lane);
     produce(b0, 0);
     for (uint32_t i = 1; i < nblk; i += 3) {
       fetch(b2, i + 1);
@@ -712,27 +741,56 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // ---- consumers ----
     const uint32_t w_q = base_w + qi;
     const uint32_t w_first = base_w + qt * QT + qg * 32;
-    bf16x8 qop[KA];
-    ws_wait_ge(&q_ready, 4);
+    // B operands of S^T: this lane's query, dims 16a + 8hh .. +7 (planes hi
+    // and, for SPLIT, lo).
+    constexpr int QPL = SPLIT ? 2 : 1;
+    bf16x8 qop[QPL][KA];
+    if constexpr (SPLIT) {
+      // Every lane loads (a row past the tile's end reads row 0) and scales
+      // by zero when it has no query: no branch, so all loads issue at once.
+      const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
+      const float qsc = q_ok ? p.scale_log2 : 0.f;
 #pragma unroll
-    for (int a = 0; a < KA; ++a)
-      qop[a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
+      for (int a = 0; a < KA; ++a) {
+        const float4 x0 = scale4(ld4(qrow + a * 16 + hh * 8), qsc);
+        const float4 x1 = scale4(ld4(qrow + a * 16 + hh * 8 + 4), qsc);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const __bf16 hi = (__bf16)xs[e];
+          qop[0][a][e] = hi;
+          qop[QPL - 1][a][e] = bf16_lo(xs[e], hi);
+        }
+      }
+    } else {
+      ws_wait_ge(&q_ready, 4);
+#pragma unroll
+      for (int a = 0; a < KA; ++a)
+        qop[0][a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
+    }
     for (uint32_t i = 0; i < nblk; ++i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&filled[s], 4 * (use + 1));
       const Stage& sg = st[s];
       const uint32_t k0 = i * KB + ks * 32;
       f32x16 sc;
-      {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+#pragma unroll
+      for (int pl = 0; pl < QPL; ++pl) {
+        // K plane pl against Q hi, and (SPLIT, K hi only) against Q lo.
         bf16x8 kop[KA];
 #pragma unroll
         for (int a = 0; a < KA; ++a)
-          kop[a] = *reinterpret_cast<const bf16x8*>(&sg.ks[(ks * 32 + l32) * KP + a * 16 + hh * 8]);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+          kop[a] = *reinterpret_cast<const bf16x8*>(&sg.ks[pl][(ks * 32 + l32) * KP + a * 16 + hh * 8]);
 #pragma unroll
         for (int a = 0; a < KA; ++a)
-          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[a], sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[0][a], sc, 0, 0, 0);
+        if (SPLIT && pl == 0) {
+#pragma unroll
+          for (int a = 0; a < KA; ++a)
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[QPL - 1][a], sc, 0, 0, 0);
+        }
       }
 
       const bool unmasked = k0 + 31 < kend && k0 + 31 <= w_first;
@@ -766,25 +824,36 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
 #pragma unroll
         for (int t = 0; t < OT; ++t) o[t] *= alpha;
       }
-      bf16x8 pb[2];
+      bf16x8 pb[QPL][2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)sc[8 * c + j];
+        for (int j = 0; j < 8; ++j) {
+          const __bf16 hi = (__bf16)sc[8 * c + j];
+          pb[0][c][j] = hi;
+          if constexpr (SPLIT) pb[QPL - 1][c][j] = bf16_lo(sc[8 * c + j], hi);
+        }
       // V^T operands are read per output tile after the softmax (the stage
       // stays claimed until they are in registers), then the stage is released.
 #pragma unroll
       for (int t = 0; t < OT; ++t) {
-        bf16x8 vop[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int d = 32 * t + l32;
-          const int oct = (ks * 4 + 2 * c + hh) ^ ((d >> 2) & 7);
-          vop[c] = *reinterpret_cast<const bf16x8*>(&sg.vt[d * VP + oct * 8]);
+        for (int pl = 0; pl < QPL; ++pl) {
+          // V plane pl against P hi, and (SPLIT, V hi only) against P lo.
+          bf16x8 vop[2];
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int d = 32 * t + l32;
+            const int oct = (ks * 4 + 2 * c + hh) ^ ((d >> 2) & 7);
+            vop[c] = *reinterpret_cast<const bf16x8*>(&sg.vt[pl][d * VP + oct * 8]);
+          }
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[c], pb[0][c], o[t], 0, 0, 0);
+            if (SPLIT && pl == 0)
+              o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[c], pb[QPL - 1][c], o[t], 0, 0, 0);
+          }
         }
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-          o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[c], pb[c], o[t], 0, 0, 0);
       }
       ws_signal(&released[s], lane);
     }
@@ -826,13 +895,13 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     }
 }
 
-template <int D>
+template <int D, bool SPLIT>
 int launch_ws(const PrefillParams& p, hipStream_t stream) {
   const uint32_t nqt = (p.S + 63) / 64;
   if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
   if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
-  hipLaunchKernelGGL((prefill_ws_kernel<D>), dim3(p.H, nqt, 1), dim3(512), 0, stream, p);
+  hipLaunchKernelGGL((prefill_ws_kernel<D, SPLIT>), dim3(p.H, nqt, 1), dim3(512), 0, stream, p);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }
@@ -867,10 +936,17 @@ int launch_f32(const PrefillParams& p, hipStream_t stream) {
 }  // namespace
 
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream) {
-  const bool bf16 = precision == STS_PREC_BF16_MFMA;
-  if (head_dim == 128) return bf16 ? launch_ws<128>(p, stream) : launch_f32<128>(p, stream);
-  if (head_dim == 64) return bf16 ? launch_ws<64>(p, stream) : launch_f32<64>(p, stream);
-  return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  if (head_dim != 128 && head_dim != 64)
+    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  const bool d128 = head_dim == 128;
+  switch (precision) {
+    case STS_PREC_BF16_MFMA:
+      return d128 ? launch_ws<128, false>(p, stream) : launch_ws<64, false>(p, stream);
+    case STS_PREC_F32_SPLIT_BF16:
+      return d128 ? launch_ws<128, true>(p, stream) : launch_ws<64, true>(p, stream);
+    default:
+      return d128 ? launch_f32<128>(p, stream) : launch_f32<64>(p, stream);
+  }
 }
 
 }  // namespace sts

@@ -34,6 +34,7 @@ STS_ERR_STATE = -3
 STS_ERR_NOMEM = -4
 PREC_F32 = 0
 PREC_BF16_MFMA = 1
+PREC_F32_SPLIT_BF16 = 2
 
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32

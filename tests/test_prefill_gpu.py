@@ -1,7 +1,8 @@
 """Chunked causal prefill on the GPU against the oracle.
 
 f32 variant within 1e-4 of the oracle; bf16-MFMA variant within 2e-2 (the
-north star's bars).  The reference executes a prefill as S sequential
+north star's bars); the split-bf16 variant (three bf16 products per f32
+product) is held to the f32 bar.  The reference executes a prefill as S sequential
 decodes (stream.rs:482-492), so the chunked result is also checked against
 the GPU's own decode over each query's prefix.
 """
@@ -20,6 +21,11 @@ pytestmark = pytest.mark.gpu
 
 TOL_F32 = 1e-4
 TOL_BF16 = 2e-2
+PRECS = [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA, sts_attn.PREC_F32_SPLIT_BF16]
+
+
+def tol(prec):
+    return TOL_BF16 if prec == sts_attn.PREC_BF16_MFMA else TOL_F32
 
 
 def dev(x):
@@ -46,6 +52,9 @@ def test_prefill_fixtures(gpu, name):
     assert np.abs(got - f["out_wgsl"]).max() < TOL_F32
     got = run(q, kc, vc, args[6], L, float(f["scale"]), sts_attn.PREC_BF16_MFMA)
     assert np.abs(got - f["out_f64"]).max() < TOL_BF16
+    got = run(q, kc, vc, args[6], L, float(f["scale"]), sts_attn.PREC_F32_SPLIT_BF16)
+    assert np.abs(got - f["out_f64"]).max() < TOL_F32
+    assert np.abs(got - f["out_wgsl"]).max() < TOL_F32
 
 
 @pytest.mark.parametrize("H,D,M,cached,S,start", [
@@ -57,7 +66,7 @@ def test_prefill_fixtures(gpu, name):
     (1, 128, 3000, 2000, 130, 5),     # few tiles: key range split four ways
     (2, 64, 4096, 3000, 70, 4000),    # long wrapped window, split key range
 ])
-@pytest.mark.parametrize("prec", [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA])
+@pytest.mark.parametrize("prec", PRECS)
 def test_prefill_against_f64(gpu, H, D, M, cached, S, start, prec):
     q, kc, vc = prefill_inputs(4000 + S, H, D, M, cached, S, start)
     L = cached + S
@@ -65,7 +74,7 @@ def test_prefill_against_f64(gpu, H, D, M, cached, S, start, prec):
     ref = oracle.prefill_f64(q, kc, vc, start, L, scale_for(D))
     err = np.abs(got - ref).max()
     print(f"prefill H{H} D{D} S{S} cached{cached} prec{prec}: max-abs {err:.2e}", flush=True)
-    assert err < (TOL_F32 if prec == sts_attn.PREC_F32 else TOL_BF16)
+    assert err < tol(prec)
 
 
 def test_chunked_equals_sequential_decode_on_gpu(gpu):
@@ -105,7 +114,7 @@ def test_kv_prefill_appends_and_attends(gpu):
         assert np.abs(got - ref).max() < TOL_F32, it
 
 
-@pytest.mark.parametrize("prec", [sts_attn.PREC_F32, sts_attn.PREC_BF16_MFMA])
+@pytest.mark.parametrize("prec", PRECS)
 def test_prefill_bit_repeatable_across_split_merges(gpu, prec):
     """Split key ranges merge in split order whichever workgroup arrives last:
     repeated launches, interleaved with split decodes that share the same
@@ -124,4 +133,4 @@ def test_prefill_bit_repeatable_across_split_merges(gpu, prec):
         got = host(sts_attn.prefill_attention(qd, kd, vd, start, L, scale_for(D), prec))
         np.testing.assert_array_equal(got, first)
     ref = oracle.prefill_f64(q, kc, vc, start, L, scale_for(D))
-    assert np.abs(first - ref).max() < (TOL_F32 if prec == sts_attn.PREC_F32 else TOL_BF16)
+    assert np.abs(first - ref).max() < tol(prec)
