@@ -19,7 +19,9 @@
 //   them in split order.
 //
 //   prefill_ws_kernel (bf16 MFMA, f32 softmax and accumulation): specialised
-//   producer and consumer waves, described above the kernel.
+//   producer and consumer waves, described above the kernel.  Its SPLIT
+//   instance is the f32-accurate variant: operands split into bf16 hi and lo
+//   parts, three bf16 products per f32 product.
 //
 // Blocks are indexed (head, q-tile[, split]) with head fastest, so all
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
