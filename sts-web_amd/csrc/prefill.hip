@@ -123,7 +123,6 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   for (int a = 0; a < QN; ++a) {
     // dims 16a + 4g .. +3 (instruction (a, j) contracts dim 16a + 4g + j)
     qop[a] = scale4(ld4(qrow + a * 16 + g * 4), qs);
-  
   }
 
   float m = -FLT_MAX;
@@ -661,18 +660,17 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // Four values rounded to bf16 at one offset of the hi plane (and, for
     // SPLIT, their remainders in the lo plane).
     auto store4 = [&](__bf16* hi_plane, __bf16* lo_plane, int off, float a, float b, float c, float d) {
-      bf16x4 yh, yl;
+      bf16x4 yh;
+      yh[0] = (__bf16)a; yh[1] = (__bf16)b; yh[2] = (__bf16)c; yh[3] = (__bf16)d;
+      *reinterpret_cast<bf16x4*>(&hi_plane[off]) = yh;
       if constexpr (SPLIT) {
-        yh[0] = (__bf16)a; yh[1] = (__bf16)b; yh[2] = (__bf16)c; yh[3] = (__bf16)d;
+        bf16x4 yl;
         yl[0] = bf16_lo(a, yh[0]); yl[1] = bf16_lo(b, yh[1]);
         yl[2] = bf16_lo(c, yh[2]); yl[3] = bf16_lo(d, yh[3]);
         *reinterpret_cast<bf16x4*>(&lo_plane[off]) = yl;
       } else {
         (void)lo_plane;
-        (void)yl;
-        yh[0] = (__bf16)a; yh[1] = (__bf16)b; yh[2] = (__bf16)c; yh[3] = (__bf16)d;
       }
-      *reinterpret_cast<bf16x4*>(&hi_plane[off]) = yh;
     };
     auto put = [&](const Buf& bf, Stage& sg) {
 #pragma unroll
