@@ -29,6 +29,15 @@ def test_header_and_binding_agree():
     assert declared_functions() == sorted(sts_attn.SIGNATURES)
 
 
+def test_precision_constants_match_header():
+    """The binding's precision codes are the header's enum values."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    enum = dict((k, int(v)) for k, v in re.findall(r"\b(STS_PREC_[A-Z0-9_]+)\s*=\s*(\d+)", text))
+    assert enum == {"STS_PREC_F32": sts_attn.PREC_F32,
+                    "STS_PREC_BF16_MFMA": sts_attn.PREC_BF16_MFMA,
+                    "STS_PREC_F32_SPLIT_BF16": sts_attn.PREC_F32_SPLIT_BF16}
+
+
 def test_library_exports_every_declared_symbol():
     lib = sts_attn.load()
     for name in declared_functions():
