@@ -61,9 +61,12 @@ enum sts_precision {
   STS_PREC_BF16_MFMA = 1,     /* f32 inputs rounded to bf16 for MFMA, f32 accumulate */
   STS_PREC_F32_SPLIT_BF16 = 2 /* f32 inputs split into bf16 hi + lo (16 significant
                                  bits), each product as three bf16 MFMAs
-                                 (hi*hi + hi*lo + lo*hi), f32 accumulate: f32-level
-                                 results (within 1e-4 of f64 like STS_PREC_F32) on
-                                 the bf16 matrix rate.  Prefill only.            */
+                                 (hi*hi + hi*lo + lo*hi), f32 accumulate, on the
+                                 bf16 matrix rate.  The scores carry a relative
+                                 error of ~2^-16, so the result error grows with
+                                 the score range: within 1e-4 of f64 for scores of
+                                 standard deviation up to ~4 (STS_PREC_F32 stays
+                                 within 1e-4 far beyond).  Prefill only.         */
 };
 
 /* Message for the calling thread's most recent failed call ("" if none). */
