@@ -557,8 +557,8 @@ def main():
             "f32_us_per_layer": round(p["f32"]["us_per_layer"], 3),
             "f32_tflops": round(p["f32"]["tflops"], 1),
             "f32_frac_of_fp32_peak": round(p["f32"]["tflops"] / FP32_PEAK_TFLOPS, 4),
-            # f32-level results (1e-4 parity) from three bf16 MFMA products per
-            # f32 product: priced against the bf16 peak at three products per flop.
+            # f32-grade results for moderate score ranges from three bf16 MFMA
+            # products per f32 product: priced against the bf16 peak at three products per flop.
             "f32split_us_per_layer": round(p["f32split"]["us_per_layer"], 3),
             "f32split_tflops": round(p["f32split"]["tflops"], 1),
             "f32split_frac_of_mfma_peak": round(3 * p["f32split"]["tflops"] / BF16_PEAK_TFLOPS, 4)}

@@ -20,8 +20,8 @@
 //
 //   prefill_ws_kernel (bf16 MFMA, f32 softmax and accumulation): specialised
 //   producer and consumer waves, described above the kernel.  Its SPLIT
-//   instance is the f32-accurate variant: operands split into bf16 hi and lo
-//   parts, three bf16 products per f32 product.
+//   instance is the split variant: operands split into bf16 hi and lo parts,
+//   three bf16 products per f32 product (f32-grade for moderate score ranges).
 //
 // Blocks are indexed (head, q-tile[, split]) with head fastest, so all
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
@@ -535,7 +535,8 @@ __device__ __forceinline__ void ws_signal(uint32_t* ctr, int lane) {
   if (lane == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// SPLIT: the f32-accurate variant.  Every operand is split into bf16 hi and
+// SPLIT: the split variant (f32-grade while the scores' ~2^-16 relative error
+// stays small next to the tolerance).  Every operand is split into bf16 hi and
 // lo planes and each product runs as three bf16 MFMAs (hi*hi + hi*lo +
 // lo*hi, f32 accumulate; the dropped lo*lo term is 2^-16 relative), which
 // on this chip's 16:1 bf16:f32 matrix rate is ~5x the f32 MFMA rate.  Two
