@@ -1,9 +1,9 @@
 """Benchmark of the sts-web attention hot path on one MI355X.
 
 Headline: one temporal frame = 24 sequential layer
-decode steps, each a fused append + attention (sts_kv_decode_step) over a
-32-head x 128 f32 ring cache holding 3000 rows, with the write head at a
-seeded offset so reads wrap.  Every layer has its own 98 MB cache (2.36 GB,
+decode steps, each a fused RoPE + append + attention (sts_kv_decode_step)
+over a 32-head x 128 f32 ring cache holding 3000 rows, with the write head at
+a seeded offset so reads wrap.  Every layer has its own 98 MB cache (2.36 GB,
 beyond the 256 MB MALL).  Inputs are resident in HBM before timing.
 
 Also reported (extra fields): decode without the append (sts_kv_attend),
@@ -90,11 +90,14 @@ def bench_decode(torch, sts, stream, steps, warmup):
     kn = torch.randn((LAYERS, 1, H, D), generator=g, device="cuda")
     vn = torch.randn((LAYERS, 1, H, D), generator=g, device="cuda")
     out = torch.empty((LAYERS, 1, H, D), device="cuda")
+    # RoPE of q and k at each cache's offset (model.rs:824): the write heads sit
+    # at offsets up to 2M, and every frame moves them by one.
+    rope = sts.RoPE(D, 2 * M + warmup + steps + 64)
 
     def frame():
         for layer in range(LAYERS):
-            caches[layer].decode_step(q[layer], kn[layer], vn[layer], scale, out=out[layer],
-                                      stream=stream)
+            caches[layer].decode_step(q[layer], kn[layer], vn[layer], scale, rope=rope,
+                                      out=out[layer], stream=stream)
 
     def frame_attend():
         for layer in range(LAYERS):
@@ -534,7 +537,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (torch.randn, seeded), inputs resident in HBM",
-        "config": {"workload": "temporal decode frame: 24 layers x fused append+attention, "
+        "config": {"workload": "temporal decode frame: 24 layers x fused RoPE+append+attention, "
                                "32 heads x 128, f32 ring KV cache of 3000 rows (wrapped), batch 1",
                    "layers": LAYERS, "heads": H, "head_dim": D, "kv_len": M},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

@@ -30,8 +30,11 @@
  *     is an error.
  *   - Attention entry points use a per-(device, stream) workspace owned by the
  *     library for split-KV partial results.  It is allocated (hipMalloc) on the
- *     first call on a stream and grown when a larger launch needs it; warm a
- *     stream up before capturing it in a HIP graph.  Calls issued on the same
+ *     first call on a stream that needs it and grown when a larger launch needs
+ *     more; replaced buffers are retired, not freed, so graphs captured earlier
+ *     stay valid.  A call that would allocate or grow it while its stream is
+ *     being captured into a HIP graph fails with STS_ERR_STATE: run the largest
+ *     call once on the stream before capturing it.  Calls issued on the same
  *     stream are ordered; calls on different streams use different workspaces.
  *   - Handles are not internally locked: use one handle from one host thread at
  *     a time (the reference's caches are !Sync, model.rs:483).
@@ -46,14 +49,22 @@
 extern "C" {
 #endif
 
-#define STS_ATTN_ABI_VERSION 1
+#define STS_ATTN_ABI_VERSION 2
 
 enum sts_status {
   STS_OK = 0,
   STS_ERR_INVALID = -1, /* bad argument: null pointer, size, head_dim, range */
   STS_ERR_HIP = -2,     /* a HIP runtime call failed (message has the code)  */
   STS_ERR_STATE = -3,   /* handle in the wrong state for the call            */
-  STS_ERR_NOMEM = -4    /* device or host allocation failed                  */
+  STS_ERR_NOMEM = -4,   /* device or host allocation failed                  */
+  STS_ERR_DEVICE = -5   /* a kernel raised a device error flag (sts_device_errors) */
+};
+
+/* Bits of the device error word (sts_device_errors). */
+enum sts_device_error {
+  STS_DEVERR_WAIT_TIMEOUT = 1 /* a bounded wait between the waves of a workgroup
+                                 gave up (bf16 prefill kernels); outputs written
+                                 since the last check are invalid               */
 };
 
 enum sts_precision {
@@ -268,14 +279,44 @@ int sts_kv_decode_step(sts_kv_cache* cache, const sts_rope* rope, const float* q
                        uint64_t batch, float scale, void* stream);
 
 /*
- * Chunked prefill (batch 1): append `seq` rows of k_new/v_new
- * ([seq][heads][head_dim], RoPE already applied) and run causal attention of
- * the `seq` queries q [seq][heads][head_dim] over the grown window into out.
- * The prefill branch of model.rs:760-797 with a working multi-row append.
+ * Chunked prefill (batch 1): the prefill branch of
+ * Q4Attention::forward_with_cache (model.rs:760-797) with a working
+ * multi-row append.  With `rope` set, q and k_new are read unrotated and
+ * rotated at positions offset..offset+seq-1 (RoPE::apply, model.rs:760-764):
+ * k inside the append, which writes the K and V rows
+ * ([seq][heads][head_dim]) at slots (offset+s) % max_len in one launch, and q
+ * in registers inside the attention kernel (the rotated q is not written
+ * back).  With rope NULL, q and k_new are taken as already rotated.  Then
+ * causal attention of the `seq` queries q [seq][heads][head_dim] over the
+ * grown window into out.  Every argument is checked before anything is
+ * written: a rejected call leaves the cache and its counters unchanged.
+ * q, k_new, v_new, out 16-byte aligned; offset+seq must not exceed the RoPE
+ * table.
  */
-int sts_kv_prefill(sts_kv_cache* cache, const float* q, const float* k_new,
-                   const float* v_new, float* out, uint64_t seq, float scale,
-                   int precision, void* stream);
+int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
+                   const float* k_new, const float* v_new, float* out, uint64_t seq,
+                   float scale, int precision, void* stream);
+
+/* ---- device error word ---------------------------------------------------- */
+
+/*
+ * Synchronises `stream`, then reads and clears the current device's error
+ * word (STS_DEVERR_* bits raised by kernels since the last call, on any
+ * stream) into *flags (may be NULL).  Returns STS_ERR_DEVICE when a bit was
+ * set.  No counterpart in the reference: its WGSL shaders have no bounded
+ * waits.  The bf16 prefill kernels' waves hand over LDS stages through
+ * bounded polls; a poll that gives up sets STS_DEVERR_WAIT_TIMEOUT instead of
+ * hanging the GPU.
+ */
+int sts_device_errors(void* stream, uint32_t* flags);
+
+/*
+ * Test hook, no counterpart in the reference: the number of polls after which
+ * the bounded waits give up (0 restores the default, 2^24).  A small value
+ * makes the waits give up on purpose so that tests can check that the error
+ * word reports it while every kernel still exits normally.
+ */
+int sts_debug_set_wait_limit(uint32_t polls);
 
 /* ---- Q4_K projections (the matvecs on either side of attention) --------- */
 

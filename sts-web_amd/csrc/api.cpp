@@ -209,14 +209,11 @@ int sts_prefill_attention(const float* q, const float* k_cache, const float* v_c
                           void* stream) {
   sts::clear_error();
   STS_CHECK(q && k_cache && v_cache && out, "null pointer argument");
-  if (int rc = check_head_dim(head_dim)) return rc;
   STS_CHECK(heads >= 1 && max_len >= 1, "empty shape");
   STS_CHECK(seq >= 1 && seq <= win_len, "need 1 <= seq (%u) <= win_len (%u)", seq, win_len);
   STS_CHECK(win_len <= max_len, "win_len %u > max_len %u", win_len, max_len);
   STS_CHECK(win_start < max_len, "win_start %u >= max_len %u", win_start, max_len);
-  STS_CHECK(precision == STS_PREC_F32 || precision == STS_PREC_BF16_MFMA ||
-                precision == STS_PREC_F32_SPLIT_BF16,
-            "precision %d unknown", precision);
+  if (int rc = sts::check_prefill(seq, heads, head_dim, max_len, precision)) return rc;
   STS_CHECK(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
             "pointers must be 16-byte aligned");
   STS_CHECK(std::isfinite(scale), "scale must be finite");
@@ -383,14 +380,23 @@ int sts_kv_update(sts_kv_cache* cache, const float* k_new, const float* v_new, u
   // gpu_cache_write_v with pos_offset = offset (model.rs:747-749); write_pos
   // and offset agree modulo max_len under advance and rollback.
   const uint32_t pos = (uint32_t)(cache->offset % cache->max_len);
-  if (int rc = sts::launch_cache_write(k_new, cache->k, pos, (uint32_t)batch, (uint32_t)seq,
-                                       (uint32_t)cache->heads, (uint32_t)cache->head_dim,
-                                       (uint32_t)cache->max_len, s))
-    return rc;
-  if (int rc = sts::launch_cache_write(v_new, cache->v, pos, (uint32_t)batch, (uint32_t)seq,
-                                       (uint32_t)cache->heads, (uint32_t)cache->head_dim,
-                                       (uint32_t)cache->max_len, s))
-    return rc;
+  if (aligned16(k_new) && aligned16(v_new)) {
+    // K and V in one launch.
+    if (int rc = sts::launch_kv_append(k_new, v_new, cache->k, cache->v, pos, (uint32_t)batch,
+                                       (uint32_t)seq, (uint32_t)cache->heads,
+                                       (uint32_t)cache->head_dim, (uint32_t)cache->max_len,
+                                       nullptr, nullptr, 0, s))
+      return rc;
+  } else {
+    if (int rc = sts::launch_cache_write(k_new, cache->k, pos, (uint32_t)batch, (uint32_t)seq,
+                                         (uint32_t)cache->heads, (uint32_t)cache->head_dim,
+                                         (uint32_t)cache->max_len, s))
+      return rc;
+    if (int rc = sts::launch_cache_write(v_new, cache->v, pos, (uint32_t)batch, (uint32_t)seq,
+                                         (uint32_t)cache->heads, (uint32_t)cache->head_dim,
+                                         (uint32_t)cache->max_len, s))
+      return rc;
+  }
   kv_advance(cache, seq);
   return STS_OK;
 }
@@ -503,33 +509,87 @@ int sts_kv_decode_step(sts_kv_cache* cache, const sts_rope* rope, const float* q
   return STS_OK;
 }
 
-int sts_kv_prefill(sts_kv_cache* cache, const float* q, const float* k_new, const float* v_new,
-                   float* out, uint64_t seq, float scale, int precision, void* stream) {
+int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
+                   const float* k_new, const float* v_new, float* out, uint64_t seq,
+                   float scale, int precision, void* stream) {
   sts::clear_error();
+  // Every check runs before anything is written or the counters move, so a
+  // rejected call leaves the cache as it was.
   STS_CHECK(cache && q && k_new && v_new && out, "null pointer argument");
   STS_CHECK(seq >= 1 && seq <= cache->max_len, "seq %llu must be in 1..max_len",
             (unsigned long long)seq);
   if (cache->k && cache->batch != 1)
     return fail(STS_ERR_STATE, "prefill needs a batch-1 cache (allocated with batch %llu)",
                 (unsigned long long)cache->batch);
+  if (int rc = sts::check_prefill((uint32_t)seq, (uint32_t)cache->heads,
+                                  (uint32_t)cache->head_dim, (uint32_t)cache->max_len, precision))
+    return rc;
+  STS_CHECK(aligned16(q) && aligned16(k_new) && aligned16(v_new) && aligned16(out),
+            "q, k_new, v_new, out must be 16-byte aligned");
+  STS_CHECK(std::isfinite(scale), "scale must be finite");
+  if (rope) {
+    STS_CHECK(rope->head_dim == cache->head_dim, "RoPE head_dim %u != cache head_dim %llu",
+              rope->head_dim, (unsigned long long)cache->head_dim);
+    // RoPE::apply slices the table at offset..offset+seq (model.rs:92-95).
+    STS_CHECK(cache->offset + seq <= rope->max_seq_len,
+              "positions %llu..%llu beyond the RoPE table (%u rows)",
+              (unsigned long long)cache->offset, (unsigned long long)(cache->offset + seq),
+              rope->max_seq_len);
+  }
   hipStream_t s = as_stream(stream);
   if (int rc = kv_ensure(cache, 1, s)) return rc;
   sts_kv_cache next = *cache;
   kv_advance(&next, seq);
   const uint32_t pos = (uint32_t)(cache->offset % cache->max_len);
-  if (int rc = sts::launch_cache_write(k_new, cache->k, pos, 1, (uint32_t)seq,
-                                       (uint32_t)cache->heads, (uint32_t)cache->head_dim,
-                                       (uint32_t)cache->max_len, s))
+  // RoPE of k (at offset + s) fused into one append launch of K and V.
+  if (int rc = sts::launch_kv_append(k_new, v_new, cache->k, cache->v, pos, 1, (uint32_t)seq,
+                                     (uint32_t)cache->heads, (uint32_t)cache->head_dim,
+                                     (uint32_t)cache->max_len, rope ? rope->cos_t : nullptr,
+                                     rope ? rope->sin_t : nullptr, (uint32_t)cache->offset, s))
     return rc;
-  if (int rc = sts::launch_cache_write(v_new, cache->v, pos, 1, (uint32_t)seq,
-                                       (uint32_t)cache->heads, (uint32_t)cache->head_dim,
-                                       (uint32_t)cache->max_len, s))
-    return rc;
+  const uint64_t q_pos0 = cache->offset;
   *cache = next;
-  return sts_prefill_attention(q, cache->k, cache->v, out, (uint32_t)seq, (uint32_t)cache->heads,
-                               (uint32_t)cache->head_dim, (uint32_t)cache->max_len,
-                               (uint32_t)kv_start(cache), (uint32_t)cache->len, scale, precision,
-                               stream);
+  sts::PrefillParams p;
+  p.q = q;
+  p.k = cache->k;
+  p.v = cache->v;
+  p.out = out;
+  p.S = (uint32_t)seq;
+  p.H = (uint32_t)cache->heads;
+  p.M = (uint32_t)cache->max_len;
+  p.start = (uint32_t)kv_start(cache);
+  p.len = (uint32_t)cache->len;
+  p.scale_log2 = sts::softmax_scale_log2(scale);
+  if (rope) {
+    // q rotated in registers inside the attention kernel (table rows offset + i).
+    p.rope_cos = rope->cos_t;
+    p.rope_sin = rope->sin_t;
+    p.rope_pos0 = (uint32_t)q_pos0;
+  }
+  return sts::launch_prefill(p, (uint32_t)cache->head_dim, precision, s);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Device error word and wait bound                                         */
+/* ---------------------------------------------------------------------- */
+
+int sts_device_errors(void* stream, uint32_t* flags) {
+  sts::clear_error();
+  uint32_t f = 0;
+  if (int rc = sts::take_prefill_errors(as_stream(stream), &f)) return rc;
+  if (flags) *flags = f;
+  if (f & STS_DEVERR_WAIT_TIMEOUT)
+    return fail(STS_ERR_DEVICE,
+                "a bounded wait inside a kernel gave up (flags 0x%x): an output written since "
+                "the last check is invalid", f);
+  if (f) return fail(STS_ERR_DEVICE, "device error flags 0x%x", f);
+  return STS_OK;
+}
+
+int sts_debug_set_wait_limit(uint32_t polls) {
+  sts::clear_error();
+  sts::set_wait_limit(polls);
+  return STS_OK;
 }
 
 }  // extern "C"

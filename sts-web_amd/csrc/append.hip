@@ -6,6 +6,7 @@
 // replaces RoPE::apply_rope_to_tensor (crates/sts-wasm/src/model.rs:79-105).
 #include "append.hpp"
 #include "common.hpp"
+#include "rope.hpp"
 
 namespace sts {
 
@@ -48,28 +49,53 @@ __global__ __launch_bounds__(256) void cache_write_scalar(const float* __restric
   cache[((b * H + h) * max_len + slot) * D + d] = in[i];
 }
 
+// K and V appended in one launch: one thread per 4 consecutive elements of
+// k_in / v_in [B][S][H][D] (D % 4 == 0) writes them to slot
+// (pos_offset + s) % max_len of their caches, the K row rotated first at
+// table row rope_pos0 + s when cos_t is set (RoPE then cache write, as
+// model.rs:760-764 runs them).
+__global__ __launch_bounds__(256) void kv_append_vec4(const float4* __restrict__ k_in,
+                                                      const float4* __restrict__ v_in,
+                                                      float4* __restrict__ k_cache,
+                                                      float4* __restrict__ v_cache,
+                                                      const float2* __restrict__ cos_t,
+                                                      const float2* __restrict__ sin_t,
+                                                      uint32_t rope_pos0, uint32_t pos_offset,
+                                                      uint32_t S, uint32_t H, uint32_t D4,
+                                                      uint32_t max_len, uint64_t total4) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total4) return;
+  const uint32_t d4 = (uint32_t)(i % D4);
+  const uint64_t rem = i / D4;
+  const uint32_t h = (uint32_t)(rem % H);
+  const uint64_t rem2 = rem / H;
+  const uint32_t s = (uint32_t)(rem2 % S);
+  const uint64_t b = rem2 / S;
+  const uint32_t slot = (uint32_t)(((uint64_t)pos_offset + s) % max_len);
+  const uint64_t dst = ((b * H + h) * max_len + slot) * D4 + d4;
+  float4 k = k_in[i];
+  const float4 v = v_in[i];
+  if (cos_t) {
+    const uint64_t row = (uint64_t)(rope_pos0 + s) * D4 + d4;
+    k = rope4(k, cos_t[row], sin_t[row]);
+  }
+  k_cache[dst] = k;
+  v_cache[dst] = v;
+}
+
 // One thread per two adjacent rotation pairs (4 floats) of x [B][S][H][D].
 __global__ __launch_bounds__(256) void rope_kernel(float4* __restrict__ x,
                                                    const float2* __restrict__ cos_t,
                                                    const float2* __restrict__ sin_t,
                                                    uint32_t S, uint32_t H, uint32_t D4,
                                                    uint32_t offset, uint64_t total4) {
-#pragma clang fp contract(off)
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total4) return;
   const uint32_t d4 = (uint32_t)(i % D4);
   const uint32_t s = (uint32_t)((i / D4 / H) % S);
   // A table row holds D/2 floats; float2 entry d4 covers pairs 2*d4, 2*d4+1.
   const uint64_t row = (uint64_t)(offset + s) * D4 + d4;
-  const float2 c = cos_t[row];
-  const float2 sn = sin_t[row];
-  const float4 v = x[i];
-  float4 y;
-  y.x = v.x * c.x - v.y * sn.x;
-  y.y = v.x * sn.x + v.y * c.x;
-  y.z = v.z * c.y - v.w * sn.y;
-  y.w = v.z * sn.y + v.w * c.y;
-  x[i] = y;
+  x[i] = rope4(x[i], cos_t[row], sin_t[row]);
 }
 
 }  // namespace
@@ -92,6 +118,25 @@ int launch_cache_write(const float* input, float* cache, uint32_t pos_offset, ui
     hipLaunchKernelGGL(cache_write_scalar, dim3((uint32_t)blocks), dim3(256), 0, stream, input,
                        cache, pos_offset, seq, heads, head_dim, max_len, total);
   }
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+int launch_kv_append(const float* k_in, const float* v_in, float* k_cache, float* v_cache,
+                     uint32_t pos_offset, uint32_t batch, uint32_t seq, uint32_t heads,
+                     uint32_t head_dim, uint32_t max_len, const float* cos_t, const float* sin_t,
+                     uint32_t rope_pos0, hipStream_t stream) {
+  const uint64_t total4 = (uint64_t)batch * seq * heads * head_dim / 4;
+  if (total4 == 0) return STS_OK;
+  if (head_dim % 4 != 0 || ((uintptr_t)k_in | (uintptr_t)v_in | (uintptr_t)k_cache |
+                            (uintptr_t)v_cache) % 16 != 0)
+    return fail(STS_ERR_INVALID, "fused K/V append needs head_dim %% 4 == 0 and 16-byte aligned rows");
+  const uint64_t blocks = (total4 + 255) / 256;
+  hipLaunchKernelGGL(kv_append_vec4, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<const float4*>(k_in), reinterpret_cast<const float4*>(v_in),
+                     reinterpret_cast<float4*>(k_cache), reinterpret_cast<float4*>(v_cache),
+                     reinterpret_cast<const float2*>(cos_t), reinterpret_cast<const float2*>(sin_t),
+                     rope_pos0, pos_offset, seq, heads, head_dim / 4, max_len, total4);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }

@@ -1,9 +1,11 @@
 // common.cpp -- error reporting and per-(device, stream) workspace.
 #include "common.hpp"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 namespace sts {
 
@@ -12,6 +14,8 @@ thread_local std::string g_last_error;
 
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+// Workspace buffers replaced by larger ones; kept until the process ends.
+std::vector<void*> g_retired;
 
 std::mutex g_cu_mutex;
 std::map<int, int> g_cu;
@@ -37,27 +41,43 @@ int get_workspace(hipStream_t stream, size_t part_floats, size_t n_counters, Wor
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   Workspace& ws = g_ws[{dev, stream}];
   if (ws.part_floats < part_floats || ws.n_counters < n_counters) {
-    // Work already queued on this stream may still use the old buffers.
-    if (ws.part || ws.counters) STS_HIP(hipStreamSynchronize(stream));
-    if (ws.part) STS_HIP(hipFree(ws.part));
-    if (ws.counters) STS_HIP(hipFree(ws.counters));
-    ws = Workspace{};
-    size_t pf = part_floats > 0 ? part_floats : 1;
-    size_t nc = n_counters > 0 ? n_counters : 1;
-    // Round up so that slowly growing workloads do not reallocate every call.
+    // A stream being captured into a HIP graph must not allocate: the graph
+    // would record the counters' initialisation and keep pointers that the
+    // eager path could later replace.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    STS_HIP(hipStreamIsCapturing(stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(STS_ERR_STATE,
+                  "split workspace of %zu floats / %zu counters needed while the stream is "
+                  "being captured; run the call once on this stream before capturing it",
+                  part_floats, n_counters);
+    // The old buffers are retired, not freed: kernels queued on the stream
+    // and graphs captured earlier keep using them.  Growth at least doubles,
+    // so the retired buffers never exceed the live ones.
+    size_t pf = std::max(part_floats, 2 * ws.part_floats);
+    size_t nc = std::max(n_counters, 2 * ws.n_counters);
+    pf = std::max<size_t>(pf, 1);
+    nc = std::max<size_t>(nc, 1);
     pf = (pf + 65535) & ~size_t(65535);
     nc = (nc + 1023) & ~size_t(1023);
-    if (hipMalloc(&ws.part, pf * sizeof(float)) != hipSuccess) {
-      ws.part = nullptr;
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
+    if (hipMalloc(&part, pf * sizeof(float)) != hipSuccess)
       return fail(STS_ERR_NOMEM, "workspace allocation of %zu bytes failed", pf * sizeof(float));
-    }
-    if (hipMalloc(&ws.counters, nc * sizeof(uint32_t)) != hipSuccess) {
-      (void)hipFree(ws.part);
-      ws.part = nullptr;
-      ws.counters = nullptr;
+    if (hipMalloc(&counters, nc * sizeof(uint32_t)) != hipSuccess) {
+      (void)hipFree(part);
       return fail(STS_ERR_NOMEM, "workspace counter allocation failed");
     }
-    STS_HIP(hipMemsetAsync(ws.counters, 0, nc * sizeof(uint32_t), stream));
+    // The counters start at zero; every launch leaves them at zero.
+    if (hipMemsetAsync(counters, 0, nc * sizeof(uint32_t), stream) != hipSuccess) {
+      (void)hipFree(part);
+      (void)hipFree(counters);
+      return fail(STS_ERR_HIP, "workspace counter initialisation failed");
+    }
+    if (ws.part) g_retired.push_back(ws.part);
+    if (ws.counters) g_retired.push_back(ws.counters);
+    ws.part = part;
+    ws.counters = counters;
     ws.part_floats = pf;
     ws.n_counters = nc;
   }

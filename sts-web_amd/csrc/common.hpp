@@ -41,8 +41,10 @@ struct Workspace {
 };
 
 // Returns a workspace for `stream` on the current device holding at least the
-// requested sizes.  Growing synchronises the stream before freeing the old
-// buffers; new counters are zero-filled on the stream.
+// requested sizes.  Growing allocates new buffers (new counters zero-filled on
+// the stream) and retires the old ones without freeing them, so work queued
+// earlier and graphs captured earlier stay valid.  Fails with STS_ERR_STATE
+// when it would have to allocate while the stream is being captured.
 int get_workspace(hipStream_t stream, size_t part_floats, size_t n_counters, Workspace** out);
 
 // Number of compute units of the current device (cached per device).

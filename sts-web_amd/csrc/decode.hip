@@ -23,6 +23,7 @@
 #include "coherent.hpp"
 #include "decode.hpp"
 #include "lane.hpp"
+#include "rope.hpp"
 
 namespace sts {
 
@@ -39,18 +40,6 @@ __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<floa
 // K/V rows are read once per launch: nontemporal (streaming) loads keep them
 // from displacing useful lines and measure ~9% faster on this access pattern.
 constexpr int kNt = 2;  // buffer-load cache policy bit: nontemporal
-
-// Interleaved RoPE of two adjacent pairs (model.rs:99-100), each product and
-// sum rounded separately as the reference evaluates them.
-__device__ __forceinline__ float4 rope4(float4 x, float2 cs, float2 sn) {
-#pragma clang fp contract(off)
-  float4 y;
-  y.x = x.x * cs.x - x.y * sn.x;
-  y.y = x.x * sn.x + x.y * cs.x;
-  y.z = x.z * cs.y - x.w * sn.y;
-  y.w = x.z * sn.y + x.w * cs.y;
-  return y;
-}
 
 // One transposing butterfly level: N values in, N/2 out.  The lane whose bit
 // LEVEL is set keeps the upper half, its partner the lower half.
@@ -150,6 +139,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   const uint32_t nunits = (len + RPI - 1) / RPI;
 
   const size_t qoff = b * p.q_bstride + (size_t)h * D + c * 4;
+  // q is rotated and scaled before the first K/V loads are issued: issuing
+  // them first and waiting for q afterwards measured ~1 us slower per
+  // config-2 launch (20.3 vs 19.25 us), on the same box.
   float4 q4 = ld4(p.q + qoff);
   float2 rc = make_float2(0.f, 0.f), rs = make_float2(0.f, 0.f);
   const bool rope = p.rope_cos != nullptr;
@@ -179,8 +171,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   const uint32_t new_unit = new_row / RPI;
   const int new_g = (int)((new_row % RPI) % NG), new_j = (int)((new_row % RPI) / NG);
 
-  // The fused-append row: RoPE'd in registers, written to its slot once (by
-  // the wave whose unit holds it) and used from registers by that wave.
+  // The fused-append row: written to its slot once, RoPE'd, by the lanes of
+  // the wave whose unit holds it, which also use it from registers.
   float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
   if (append) {
     kn = ld4(p.k_new + qoff);
@@ -258,10 +250,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // the other way round; 3.93 vs 4.03 us per depformer step).
   auto store_new_row = [&]() {
     if (!append) return;
-    if (rope) kn = rope4(kn, rc, rs);
     const uint32_t owner_split = new_unit % nsplit;
     const uint32_t owner_wave = (new_unit / nsplit) % WAVES;
     if (split == owner_split && (uint32_t)wave == owner_wave && g == new_g) {
+      // Only these lanes wait for k_new and the table: the others go on to
+      // their first loads.
+      if (rope) kn = rope4(kn, rc, rs);
       uint32_t slot = start + new_row;
       slot = slot >= p.M ? slot - p.M : slot;
       st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);

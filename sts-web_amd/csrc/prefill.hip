@@ -27,12 +27,16 @@
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
 // L2 copy of the head's K/V; the heaviest (last) q-tiles are dispatched first.
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
+#include <map>
+#include <mutex>
 
 #include "coherent.hpp"
 #include "common.hpp"
 #include "lane.hpp"
 #include "prefill.hpp"
+#include "rope.hpp"
 
 namespace sts {
 
@@ -44,6 +48,29 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;  // queries per workgroup
 constexpr int kBK = 64;  // keys per LDS block
+
+// Error bits (STS_DEVERR_*) raised by the kernels of this file on the current
+// device, and the word take_errors_kernel moves them to for the host.
+__device__ uint32_t g_prefill_errors;
+__device__ uint32_t g_prefill_errors_taken;
+
+__global__ void take_errors_kernel() {
+  if (threadIdx.x == 0) g_prefill_errors_taken = atomicExch(&g_prefill_errors, 0u);
+}
+
+// Query row of q (scaled by zero when the lane has no query) with optional
+// RoPE at table row rope_pos0 + i: four dims d0..d0+3.
+template <int D>
+__device__ __forceinline__ float4 load_query4(const PrefillParams& p, const float* qrow,
+                                              uint32_t i, int d0, float qscale) {
+  float4 x = *reinterpret_cast<const float4*>(qrow + d0);
+  if (p.rope_cos) {
+    float2 cs, sn;
+    rope_coeffs<D>(p.rope_cos, p.rope_sin, p.rope_pos0 + i, d0, cs, sn);
+    x = rope4(x, cs, sn);
+  }
+  return make_float4(x.x * qscale, x.y * qscale, x.z * qscale, x.w * qscale);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -117,12 +144,13 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   float4 qop[QN];
   // Every lane loads (a row past the tile's end reads row 0) and scales by
   // zero when it has no query: no branch, so all loads issue at once.
-  const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
+  const uint32_t qrow_i = q_ok ? qi : 0;
+  const float* qrow = p.q + ((size_t)qrow_i * p.H + h) * D;
   const float qs = q_ok ? p.scale_log2 : 0.f;
 #pragma unroll
   for (int a = 0; a < QN; ++a) {
     // dims 16a + 4g .. +3 (instruction (a, j) contracts dim 16a + 4g + j)
-    qop[a] = scale4(ld4(qrow + a * 16 + g * 4), qs);
+    qop[a] = load_query4<D>(p, qrow, qrow_i, a * 16 + g * 4, qs);
   }
 
   float m = -FLT_MAX;
@@ -518,14 +546,19 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
 constexpr int kWaitLgkm0 = 0xC07F;
 
-// Spins until the LDS counter reaches target.  The handover is expected to
-// complete within microseconds; the bound only guarantees that every wave
-// leaves the loop.
-__device__ __forceinline__ void ws_wait_ge(const uint32_t* ctr, uint32_t target) {
-  for (uint32_t spin = 0; spin < (1u << 24); ++spin) {
-    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
-    __builtin_amdgcn_s_sleep(1);
+// Spins until the LDS counter reaches target, for at most `limit` polls.  The
+// handover completes within microseconds; the bound guarantees that every
+// wave leaves the loop.  A wait that gives up records STS_DEVERR_WAIT_TIMEOUT
+// in the device error word (the stage it goes on with may not hold its block,
+// so the output is wrong, and the host learns it from that word).
+__device__ __forceinline__ void ws_wait_ge(const uint32_t* ctr, uint32_t target, uint32_t limit,
+                                           int lane) {
+  bool done = false;
+  for (uint32_t spin = 0; spin < limit && !done; ++spin) {
+    done = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target;
+    if (!done) __builtin_amdgcn_s_sleep(1);
   }
+  if (!done && lane == 0) atomicOr(&g_prefill_errors, (uint32_t)STS_DEVERR_WAIT_TIMEOUT);
   asm volatile("" ::: "memory");
 }
 // Publishes this wave's LDS writes (or the end of its LDS reads) and counts it.
@@ -695,7 +728,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // stage's previous block (4 releases per use).
     auto produce = [&](const Buf& bf, uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
-      ws_wait_ge(&released[s], 4 * use);
+      ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane);
       put(bf, st[s]);
       ws_signal(&filled[s], lane);
     };
@@ -713,6 +746,16 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         qv[i] = ld4(p.q + ((size_t)(qq < p.S ? qq : 0) * p.H + h) * D + d4 * 4);
       }
     }
+    // RoPE coefficients of those query rows (issued with the loads).
+    float2 qcs[QPER], qsn[QPER];
+    if (!SPLIT && p.rope_cos) {
+#pragma unroll
+      for (int i = 0; i < QPER; ++i) {
+        const uint32_t qq = qt * QT + k_row(i);
+        rope_coeffs<D>(p.rope_cos, p.rope_sin, p.rope_pos0 + (qq < p.S ? qq : 0), d4 * 4, qcs[i],
+                       qsn[i]);
+      }
+    }
     Buf b0, b1, b2;
     fetch(b0, 0);
     fetch(b1, 1);
@@ -720,6 +763,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
 #pragma unroll
       for (int i = 0; i < QPER; ++i) {
         const uint32_t qq = qt * QT + k_row(i);
+        if (p.rope_cos) qv[i] = rope4(qv[i], qcs[i], qsn[i]);
         const float4 x = scale4(qv[i], qq < p.S ? p.scale_log2 : 0.f);
         bf16x4 y;
         y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
@@ -749,12 +793,13 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     if constexpr (SPLIT) {
       // Every lane loads (a row past the tile's end reads row 0) and scales
       // by zero when it has no query: no branch, so all loads issue at once.
-      const float* qrow = p.q + ((size_t)(q_ok ? qi : 0) * p.H + h) * D;
+      const uint32_t qrow_i = q_ok ? qi : 0;
+      const float* qrow = p.q + ((size_t)qrow_i * p.H + h) * D;
       const float qsc = q_ok ? p.scale_log2 : 0.f;
 #pragma unroll
       for (int a = 0; a < KA; ++a) {
-        const float4 x0 = scale4(ld4(qrow + a * 16 + hh * 8), qsc);
-        const float4 x1 = scale4(ld4(qrow + a * 16 + hh * 8 + 4), qsc);
+        const float4 x0 = load_query4<D>(p, qrow, qrow_i, a * 16 + hh * 8, qsc);
+        const float4 x1 = load_query4<D>(p, qrow, qrow_i, a * 16 + hh * 8 + 4, qsc);
         const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -764,14 +809,14 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         }
       }
     } else {
-      ws_wait_ge(&q_ready, 4);
+      ws_wait_ge(&q_ready, 4, p.wait_limit, lane);
 #pragma unroll
       for (int a = 0; a < KA; ++a)
         qop[0][a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
     }
     for (uint32_t i = 0; i < nblk; ++i) {
       const uint32_t s = i % NS, use = i / NS;
-      ws_wait_ge(&filled[s], 4 * (use + 1));
+      ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane);
       const Stage& sg = st[s];
       const uint32_t k0 = i * KB + ks * 32;
       f32x16 sc;
@@ -923,7 +968,7 @@ int launch_f32(const PrefillParams& p, hipStream_t stream) {
   q.nsplit = nsplit;
   if (nsplit > 1) {
     Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)tiles * nsplit * 256 * (D + 2), tiles, &ws);
+    const int rc = get_workspace(stream, (size_t)tiles * nsplit * 256 * (D / 4 + 2), tiles, &ws);
     if (rc != STS_OK) return rc;
     q.part = ws->part;
     q.counters = ws->counters;
@@ -936,9 +981,59 @@ int launch_f32(const PrefillParams& p, hipStream_t stream) {
 
 }  // namespace
 
-int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream) {
+namespace {
+std::atomic<uint32_t> g_wait_limit{1u << 24};
+std::mutex g_err_mutex;
+std::map<int, uint32_t*> g_err_taken;  // per device: address of g_prefill_errors_taken
+}  // namespace
+
+void set_wait_limit(uint32_t polls) { g_wait_limit = polls ? polls : (1u << 24); }
+uint32_t wait_limit() { return g_wait_limit; }
+
+int take_prefill_errors(hipStream_t stream, uint32_t* flags) {
+  int dev = 0;
+  STS_HIP(hipGetDevice(&dev));
+  uint32_t* taken = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_err_mutex);
+    auto it = g_err_taken.find(dev);
+    if (it != g_err_taken.end()) {
+      taken = it->second;
+    } else {
+      STS_HIP(hipGetSymbolAddress(reinterpret_cast<void**>(&taken),
+                                  HIP_SYMBOL(g_prefill_errors_taken)));
+      g_err_taken[dev] = taken;
+    }
+  }
+  // The word is swapped to zero on the device (no flag raised between the
+  // read and the clear is lost), after the work queued on `stream`.
+  hipLaunchKernelGGL(take_errors_kernel, dim3(1), dim3(64), 0, stream);
+  STS_HIP(hipGetLastError());
+  STS_HIP(hipStreamSynchronize(stream));
+  uint32_t v = 0;
+  STS_HIP(hipMemcpy(&v, taken, sizeof v, hipMemcpyDeviceToHost));
+  *flags = v;
+  return STS_OK;
+}
+
+int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_len,
+                  int precision) {
   if (head_dim != 128 && head_dim != 64)
     return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  if (precision != STS_PREC_F32 && precision != STS_PREC_BF16_MFMA &&
+      precision != STS_PREC_F32_SPLIT_BF16)
+    return fail(STS_ERR_INVALID, "precision %d unknown", precision);
+  if (heads < 1 || heads > 65535u) return fail(STS_ERR_INVALID, "heads %u out of 1..65535", heads);
+  if ((seq + 63u) / 64u > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", seq);
+  if ((uint64_t)max_len * head_dim * sizeof(float) > 0x7FFFFFF0ull)
+    return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", max_len);
+  return STS_OK;
+}
+
+int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hipStream_t stream) {
+  if (int rc = check_prefill(p0.S, p0.H, head_dim, p0.M, precision)) return rc;
+  PrefillParams p = p0;
+  p.wait_limit = g_wait_limit;
   const bool d128 = head_dim == 128;
   switch (precision) {
     case STS_PREC_BF16_MFMA:

@@ -24,8 +24,29 @@ struct PrefillParams {
   uint32_t nsplit = 1;
   float* part = nullptr;
   uint32_t* counters = nullptr;
+  // With rope_cos set, query i is rotated in registers at table row
+  // rope_pos0 + i before it is scaled (tables [max_pos][D/2]).
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  uint32_t rope_pos0 = 0;
+  // Polls after which a bounded wait of the bf16 kernels gives up and records
+  // STS_DEVERR_WAIT_TIMEOUT in the device error word.
+  uint32_t wait_limit = 1u << 24;
 };
 
+// Checks everything launch_prefill would reject for these sizes, without
+// launching (callers that mutate state first validate with it).
+int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_len,
+                  int precision);
+
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream);
+
+// Poll bound given to the bf16 kernels' waits (0 restores the default).
+void set_wait_limit(uint32_t polls);
+uint32_t wait_limit();
+
+// Reads and clears the prefill kernels' device error word on the current
+// device (after synchronising `stream`); *flags gets the STS_DEVERR_* bits.
+int take_prefill_errors(hipStream_t stream, uint32_t* flags);
 
 }  // namespace sts

@@ -32,6 +32,8 @@ STS_ERR_INVALID = -1
 STS_ERR_HIP = -2
 STS_ERR_STATE = -3
 STS_ERR_NOMEM = -4
+STS_ERR_DEVICE = -5
+DEVERR_WAIT_TIMEOUT = 1
 PREC_F32 = 0
 PREC_BF16_MFMA = 1
 PREC_F32_SPLIT_BF16 = 2
@@ -82,7 +84,9 @@ SIGNATURES = {
     "sts_kv_rollback": (_int, [_vp, _u64]),
     "sts_kv_attend": (_int, [_vp, _vp, _vp, _f32, _vp]),
     "sts_kv_decode_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u64, _f32, _vp]),
-    "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
+    "sts_kv_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u64, _f32, _int, _vp]),
+    "sts_device_errors": (_int, [_vp, ctypes.POINTER(_u32)]),
+    "sts_debug_set_wait_limit": (_int, [_u32]),
     "sts_q4k_matvec": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "sts_q4k_dequant": (_int, [_vp, _vp, _u32, _u32, _vp]),
     "sts_q4k_gemm": (_int, [_vp, _vp, _u64, _vp, _f32, _vp, _u64, _vp, _u64, _u32, _u32, _u32,
@@ -362,14 +366,17 @@ class KVCache:
         return out
 
     def prefill(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, scale: float,
-                precision: int = PREC_F32, out: Optional[torch.Tensor] = None,
-                stream=None) -> torch.Tensor:
-        """Appends S rows and runs causal chunk attention; tensors [S, H, D]."""
+                precision: int = PREC_F32, rope: Optional[RoPE] = None,
+                out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """Appends S rows and runs causal chunk attention; tensors [S, H, D].
+        With `rope`, q and k_new are unrotated and rotated at offset..offset+S-1
+        (the prefill branch, model.rs:760-797)."""
         S = q.shape[0]
         if out is None:
             out = torch.empty_like(q)
-        _check(load().sts_kv_prefill(self._h, _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(out), S,
-                                     scale, precision, _stream(stream)))
+        _check(load().sts_kv_prefill(self._h, rope.handle if rope is not None else None, _ptr(q),
+                                     _ptr(k_new), _ptr(v_new), _ptr(out), S, scale, precision,
+                                     _stream(stream)))
         return out
 
     def close(self):
@@ -433,6 +440,28 @@ def copy_device(ptr: int, shape: Sequence[int]) -> torch.Tensor:
     return t
 
 
+def device_errors(stream=None) -> int:
+    """Synchronises `stream`, reads and clears the device error word; raises
+    StsError (STS_ERR_DEVICE) when a kernel raised a flag, else returns 0."""
+    flags = _u32()
+    _check(load().sts_device_errors(_stream(stream), ctypes.byref(flags)))
+    return flags.value
+
+
+def take_device_errors(stream=None) -> int:
+    """The device error flags (read and cleared) without raising."""
+    flags = _u32()
+    rc = load().sts_device_errors(_stream(stream), ctypes.byref(flags))
+    if rc not in (STS_OK, STS_ERR_DEVICE):
+        _check(rc)
+    return flags.value
+
+
+def set_wait_limit(polls: int) -> None:
+    """Test hook: polls after which the kernels' bounded waits give up (0 = default)."""
+    _check(load().sts_debug_set_wait_limit(polls))
+
+
 def softmax_scale(head_dim: int) -> float:
     """head_dim^-0.5 as the reference computes it in f32 (model.rs:705)."""
     import numpy as np
@@ -445,6 +474,7 @@ def softmax_scale(head_dim: int) -> float:
 
 Q4K_BLOCK_BYTES = 144
 QK_K = 256
+GEMM_MAX_K = 4096  # sts_q4k_gemm's largest k; larger k goes through sts_q4k_matvec
 
 
 class Q4KTensor:
@@ -487,7 +517,8 @@ def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch
     """q4k_matmul / q4k_matmul_with_residual (gguf.rs:808-905): input
     [B, M, K] (or [B, K]) -> [B, M, N] = input @ W^T (+ residual).  M = 1 runs
     the matvec (the reference's single-token path), M > 1 the GEMM (its
-    prefill path)."""
+    prefill path) for K <= 4096 and the batched matvec (B*M rows) for larger K
+    (the temporal FFN's linear_out, K = 11264)."""
     n, k = weights.shape()
     if input.shape[-1] != k:
         raise StsError(STS_ERR_INVALID,
@@ -500,9 +531,9 @@ def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch
     res = None
     if residual is not None:
         res = residual.reshape(B * Mrows, n).contiguous()
-    if Mrows == 1:
-        _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out), B, k,
-                                     n, _stream(stream)))
+    if Mrows == 1 or k > GEMM_MAX_K:
+        _check(load().sts_q4k_matvec(weights.raw.data_ptr(), _ptr(x), _ptr(res), _ptr(out),
+                                     B * Mrows, k, n, _stream(stream)))
     else:
         _check(load().sts_q4k_gemm(weights.raw.data_ptr(), _ptr(x), k, None, 0.0, _ptr(res), n,
                                    _ptr(out), n, B * Mrows, k, n, 0, _stream(stream)))

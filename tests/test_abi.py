@@ -42,7 +42,19 @@ def test_library_exports_every_declared_symbol():
     lib = sts_attn.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.sts_abi_version() == 1
+    assert lib.sts_abi_version() == 2
+
+
+def test_status_constants_match_header():
+    """The binding's status and device-error codes are the header's enum values."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    enum = dict((k, int(v)) for k, v in
+                re.findall(r"\b(STS_(?:ERR|DEVERR)_[A-Z0-9_]+|STS_OK)\s*=\s*(-?\d+)", text))
+    assert enum == {"STS_OK": sts_attn.STS_OK, "STS_ERR_INVALID": sts_attn.STS_ERR_INVALID,
+                    "STS_ERR_HIP": sts_attn.STS_ERR_HIP, "STS_ERR_STATE": sts_attn.STS_ERR_STATE,
+                    "STS_ERR_NOMEM": sts_attn.STS_ERR_NOMEM,
+                    "STS_ERR_DEVICE": sts_attn.STS_ERR_DEVICE,
+                    "STS_DEVERR_WAIT_TIMEOUT": sts_attn.DEVERR_WAIT_TIMEOUT}
 
 
 def _err(rc):
@@ -95,6 +107,26 @@ def test_prefill_argument_errors():
                                  None))
     assert "precision" in _err(f(FAKE, FAKE, FAKE, FAKE, 512, 32, 128, 3000, 0, 768, 0.1, 7,
                                  None))
+
+
+def test_kv_prefill_rejects_before_any_device_work():
+    """sts_kv_prefill validates every argument before it allocates, appends or
+    moves the counters: on an unallocated cache a rejected call leaves it
+    unallocated and at offset 0."""
+    lib = sts_attn.load()
+    c = sts_attn.KVCache(64, 4, 128)
+    cases = [
+        ("precision", (None, FAKE, FAKE, FAKE, FAKE, 5, 0.1, 9)),
+        ("aligned", (None, FAKE + 4, FAKE, FAKE, FAKE, 5, 0.1, 0)),
+        ("scale", (None, FAKE, FAKE, FAKE, FAKE, 5, float("inf"), 0)),
+        ("seq", (None, FAKE, FAKE, FAKE, FAKE, 65, 0.1, 0)),
+        ("null", (None, None, FAKE, FAKE, FAKE, 5, 0.1, 0)),
+    ]
+    for word, (rope, q, k, v, out, seq, scale, prec) in cases:
+        assert word in _err(lib.sts_kv_prefill(c.handle, rope, q, k, v, out, seq, scale, prec,
+                                               None))
+        s = c.state()
+        assert (s.offset, s.len, s.write_pos, s.allocated) == (0, 0, 0, 0)
 
 
 def test_kv_handle_argument_errors():

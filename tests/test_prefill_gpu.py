@@ -152,3 +152,98 @@ def test_prefill_accuracy_envelope(gpu, amp, prec):
     err = np.abs(got - ref).max()
     print(f"prefill amp {amp} prec {prec}: max-abs {err:.2e}", flush=True)
     assert err < TOL_F32
+
+
+@pytest.mark.parametrize("prec", PRECS)
+@pytest.mark.parametrize("H,D,M,chunks", [
+    (8, 128, 300, (200, 150, 64, 1)),    # wraps on the second chunk
+    (4, 64, 129, (60, 65, 64)),
+])
+def test_kv_prefill_with_rope(gpu, prec, H, D, M, chunks):
+    """The prefill branch with RoPE (model.rs:760-797): q and k unrotated in, k
+    rotated at offset + s inside the append (one launch for K and V), q rotated
+    inside the attention kernel.  The cache rows equal the oracle's RoPE + cache
+    write bit for bit; the output is within the precision's bar of the f64
+    closed form over the oracle-rotated queries."""
+    rope = sts_attn.RoPE(D, 4096)
+    tabs = oracle.rope_tables(D, 4096)
+    c = sts_attn.KVCache(M, H, D)
+    o = oracle.KvCounters(M)
+    kref = np.zeros((1, H, M, D), np.float32)
+    vref = np.zeros((1, H, M, D), np.float32)
+    for it, S in enumerate(chunks):
+        q = oracle.normal(40 + it, (1, S, H, D))
+        k = oracle.normal(50 + it, (1, S, H, D))
+        v = oracle.normal(60 + it, (1, S, H, D))
+        qr = oracle.rope_apply(q, o.offset, tabs)[0]
+        kr = oracle.rope_apply(k, o.offset, tabs)
+        got = host(c.prefill(dev(q[0]), dev(k[0]), dev(v[0]), scale_for(D), prec, rope=rope))
+        oracle.cache_write(kr, kref, o.offset % M, M)
+        oracle.cache_write(v, vref, o.offset % M, M)
+        o.advance(S)
+        kb, vb = c.read_buffers()
+        np.testing.assert_array_equal(host(kb), kref)
+        np.testing.assert_array_equal(host(vb), vref)
+        ref = oracle.prefill_f64(qr, kref[0], vref[0], o.window_start(), o.len, scale_for(D))
+        err = np.abs(got - ref).max()
+        assert err < tol(prec), (it, err)
+    sts_attn.device_errors()
+
+
+def test_kv_prefill_rope_equals_prerotated(gpu):
+    """Rotating inside the kernels gives the same bits as rotating first
+    (RoPE.apply) and passing rope=None."""
+    H, D, M, S = 32, 128, 3000, 512
+    rope = sts_attn.RoPE(D, 4096)
+    for prec in PRECS:
+        a = sts_attn.KVCache(M, H, D)
+        b = sts_attn.KVCache(M, H, D)
+        for c in (a, b):
+            c.advance(2900)
+            c.update(dev(oracle.normal(5, (1, 256, H, D))), dev(oracle.normal(6, (1, 256, H, D))))
+        q = dev(oracle.normal(7, (S, H, D)))
+        k = dev(oracle.normal(8, (S, H, D)))
+        v = dev(oracle.normal(9, (S, H, D)))
+        got = host(a.prefill(q, k, v, scale_for(D), prec, rope=rope))
+        qr, kr = rope.apply(q[None], k[None], b.offset())
+        want = host(b.prefill(qr[0].contiguous(), kr[0].contiguous(), v, scale_for(D), prec))
+        np.testing.assert_array_equal(got, want)
+        ka, va = a.read_buffers()
+        kb, vb = b.read_buffers()
+        np.testing.assert_array_equal(host(ka), host(kb))
+        np.testing.assert_array_equal(host(va), host(vb))
+
+
+def test_kv_prefill_rejected_call_leaves_cache_unchanged(gpu):
+    """Every argument is checked before the append: a rejected prefill writes
+    nothing and does not move the counters."""
+    H, D, M = 4, 128, 64
+    c = sts_attn.KVCache(M, H, D)
+    c.update(dev(oracle.normal(1, (1, 10, H, D))), dev(oracle.normal(2, (1, 10, H, D))))
+    before = c.state()
+    kb0, vb0 = (host(t) for t in c.read_buffers())
+    q = dev(oracle.normal(3, (5, H, D)))
+    k = dev(oracle.normal(4, (5, H, D)))
+    v = dev(oracle.normal(5, (5, H, D)))
+    out = torch.empty_like(q)
+    lib = sts_attn.load()
+    bad_q = torch.empty(5 * H * D + 1, device="cuda")[1:]   # misaligned by 4 bytes
+    rope_short = sts_attn.RoPE(D, 12)                        # offset 10 + 5 > 12 rows
+    rope_d64 = sts_attn.RoPE(64, 4096)
+    cases = [
+        (None, q, 9, 1.0),                         # unknown precision
+        (None, bad_q, sts_attn.PREC_F32, 1.0),      # misaligned q
+        (None, q, sts_attn.PREC_F32, float("nan")),  # scale not finite
+        (rope_short, q, sts_attn.PREC_F32, 1.0),    # positions beyond the table
+        (rope_d64, q, sts_attn.PREC_F32, 1.0),      # head_dim mismatch
+    ]
+    for rope, qq, prec, scale in cases:
+        rc = lib.sts_kv_prefill(c.handle, rope.handle if rope else None, qq.data_ptr(),
+                                k.data_ptr(), v.data_ptr(), out.data_ptr(), 5, scale, prec, None)
+        assert rc == sts_attn.STS_ERR_INVALID, (prec, scale)
+        after = c.state()
+        assert (after.offset, after.len, after.write_pos) == (before.offset, before.len,
+                                                              before.write_pos)
+    kb1, vb1 = (host(t) for t in c.read_buffers())
+    np.testing.assert_array_equal(kb1, kb0)
+    np.testing.assert_array_equal(vb1, vb0)

@@ -128,3 +128,26 @@ def test_matvec_argument_errors(gpu):
                               None) == sts_attn.STS_ERR_INVALID  # misaligned weights
     with pytest.raises(sts_attn.StsError):
         sts_attn.Q4KTensor.from_q4k_bytes(blocks[:-1], (4, 512))
+
+
+@pytest.mark.parametrize("N,K,B,Mrows,residual", [(4096, 11264, 1, 5, True), (64, 11264, 2, 3, False),
+                                                  (300, 1024, 1, 7, True)])
+def test_matmul_many_rows(gpu, N, K, B, Mrows, residual):
+    """q4k_matmul with M > 1 (the reference's prefill route, gguf.rs:810-897):
+    K <= 4096 runs the GEMM, larger K (the temporal FFN's linear_out, K = 11264)
+    the batched matvec over B*M rows; both within the f32 bound of the f64
+    product, with and without the residual (gguf.rs:899-905)."""
+    blocks = oracle.q4k_random_blocks(N + K + Mrows, N, K)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    x = oracle.normal(N + 3 * Mrows, (B, Mrows, K))
+    res = oracle.normal(N + 5, (B, Mrows, N)) if residual else None
+    got = host(sts_attn.q4k_matmul(dev(x), w, residual=dev(res) if residual else None))
+    assert got.shape == (B, Mrows, N)
+    xf = x.reshape(B * Mrows, K)
+    ref = oracle.q4k_matvec_f64(blocks, xf, N)
+    tol = 1e-5 * bound(blocks, xf, N)
+    if residual:
+        r = res.reshape(B * Mrows, N).astype(np.float64)
+        ref = ref + r
+        tol = tol + 1e-6 * np.abs(r)
+    assert (np.abs(got.reshape(B * Mrows, N).astype(np.float64) - ref) <= tol).all()
