@@ -137,6 +137,26 @@ int sts_decode_ring(const float* q, const float* k_cache, const float* v_cache,
                     float scale, void* stream);
 
 /*
+ * sts_decode_ring without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, checks and results (bit for bit) as sts_decode_ring; the split
+ * partial records and arrival counters live in a static device array of the
+ * library (8 MiB of records and 16384 counters, per GPU, held until the
+ * process ends) instead of the per-stream workspace.  It calls no hipMalloc,
+ * hipFree or allocating routine.  A launch that needs more than that array
+ * holds (batch * heads * nsplit * (head_dim + 4) floats, nsplit up to 64 and
+ * chosen as sts_decode_ring chooses it; e.g. 64 streams x 32 heads x 3000
+ * rows fits) fails with STS_ERR_INVALID.  Every call on a GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (two streams, or a replayed
+ * graph beside an eager call) race and must not be issued.
+ */
+int sts_decode_ring_noalloc(const float* q, const float* k_cache, const float* v_cache,
+                            float* out, const int32_t* lens, const int32_t* starts,
+                            uint32_t batch, uint32_t heads, uint32_t head_dim,
+                            uint32_t max_len, float scale, void* stream);
+
+/*
  * Depformer step attention, batched over independent streams: appends the
  * step's K/V row at slot `step` and attends over slots 0..step (L = step+1),
  * in one launch.  Replaces the per-step cache-write K, cache-write V and

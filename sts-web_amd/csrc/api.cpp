@@ -140,9 +140,15 @@ int sts_cache_write(const float* input, float* cache, uint32_t pos_offset, uint3
                                  as_stream(stream));
 }
 
-int sts_decode_ring(const float* q, const float* k_cache, const float* v_cache, float* out,
-                    const int32_t* lens, const int32_t* starts, uint32_t batch, uint32_t heads,
-                    uint32_t head_dim, uint32_t max_len, float scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// sts_decode_ring and its allocation-free variant: same checks, same launch
+// plan; only where the split workspace lives differs.
+int decode_ring(const float* q, const float* k_cache, const float* v_cache, float* out,
+                const int32_t* lens, const int32_t* starts, uint32_t batch, uint32_t heads,
+                uint32_t head_dim, uint32_t max_len, float scale, void* stream, bool noalloc) {
   sts::clear_error();
   STS_CHECK(q && k_cache && v_cache && out && lens && starts, "null pointer argument");
   if (int rc = check_head_dim(head_dim)) return rc;
@@ -164,7 +170,27 @@ int sts_decode_ring(const float* q, const float* k_cache, const float* v_cache, 
   p.kv_hstride = (uint64_t)max_len * head_dim;
   p.kv_bstride = (uint64_t)heads * max_len * head_dim;
   p.scale_log2 = sts::softmax_scale_log2(scale);
-  return sts::launch_decode(p, batch, head_dim, max_len, as_stream(stream));
+  return noalloc ? sts::launch_decode_noalloc(p, batch, head_dim, max_len, as_stream(stream))
+                 : sts::launch_decode(p, batch, head_dim, max_len, as_stream(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int sts_decode_ring(const float* q, const float* k_cache, const float* v_cache, float* out,
+                    const int32_t* lens, const int32_t* starts, uint32_t batch, uint32_t heads,
+                    uint32_t head_dim, uint32_t max_len, float scale, void* stream) {
+  return decode_ring(q, k_cache, v_cache, out, lens, starts, batch, heads, head_dim, max_len,
+                     scale, stream, false);
+}
+
+int sts_decode_ring_noalloc(const float* q, const float* k_cache, const float* v_cache,
+                            float* out, const int32_t* lens, const int32_t* starts,
+                            uint32_t batch, uint32_t heads, uint32_t head_dim, uint32_t max_len,
+                            float scale, void* stream) {
+  return decode_ring(q, k_cache, v_cache, out, lens, starts, batch, heads, head_dim, max_len,
+                     scale, stream, true);
 }
 
 int sts_depformer_step(const float* q, const float* k_new, const float* v_new,

@@ -18,6 +18,8 @@
 // Softmax uses exp(x) = 2^(x log2 e): q is pre-multiplied by scale*log2(e) and
 // the hardware base-2 exponential is applied to (s - m) <= 0.
 #include <cfloat>
+#include <map>
+#include <mutex>
 
 #include "common.hpp"
 #include "coherent.hpp"
@@ -431,72 +433,163 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
 
 }  // namespace
 
-int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
-                  hipStream_t stream) {
+namespace {
+
+struct DecodePlan {
+  uint32_t chunk = 0;   // rows per split
+  uint32_t nsplit = 1;  // grid x
+  int waves = 1;        // waves per workgroup
+};
+
+// Chooses chunk / nsplit / waves for `units` (stream, head) pairs whose
+// longest window is max_rows.
+DecodePlan plan_decode(uint64_t units, uint32_t max_rows) {
   constexpr uint32_t kRpi = 16;
-  const uint64_t units = (uint64_t)batch * p.H;
-  if (units == 0) return STS_OK;
+  DecodePlan pl;
   // Small windows (depformer) run one wave per (stream, head); long windows
   // use 4-wave workgroups and as many splits as it takes to give the chip
   // about `target` workgroups, with chunks of 64..512 rows.
   const bool small = max_rows <= 64;
-  const int waves = small ? 1 : 4;
-  const uint32_t unit_rows = waves * kRpi;
-  uint32_t chunk, nsplit;
+  pl.waves = small ? 1 : 4;
+  const uint32_t unit_rows = pl.waves * kRpi;
   if (small) {
-    chunk = (max_rows + kRpi - 1) / kRpi * kRpi;
-    if (chunk == 0) chunk = kRpi;
-    nsplit = 1;
-  } else {
-    // One workgroup per CU (2-4 per CU measured slower: more partials to
-    // merge, no more bytes in flight per CU).
-    constexpr int chunk_max = 512, chunk_min = 64;
-    const uint64_t target = (uint64_t)device_cu_count();
-    uint64_t want = (target + units - 1) / units;
-    if (want < 1) want = 1;
-    uint64_t c = (max_rows + want - 1) / want;
-    c = (c + unit_rows - 1) / unit_rows * unit_rows;
-    if (c > (uint64_t)chunk_max) c = (uint64_t)chunk_max / unit_rows * unit_rows;
-    if (c < (uint64_t)chunk_min) c = (uint64_t)chunk_min;
-    if (c < unit_rows) c = unit_rows;
-    chunk = (uint32_t)c;
-    nsplit = (max_rows + chunk - 1) / chunk;
-    if (nsplit > (uint32_t)kMaxSplits) {
-      chunk = (max_rows + kMaxSplits - 1) / kMaxSplits;
-      chunk = (chunk + unit_rows - 1) / unit_rows * unit_rows;
-      nsplit = (max_rows + chunk - 1) / chunk;
-    }
+    pl.chunk = (max_rows + kRpi - 1) / kRpi * kRpi;
+    if (pl.chunk == 0) pl.chunk = kRpi;
+    pl.nsplit = 1;
+    return pl;
   }
-  p.chunk = chunk;
-  p.nsplit_max = nsplit;
-  if (nsplit > 1) {
-    // Partials and arrival counters.
-    Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)units * nsplit * (head_dim + 4), units, &ws);
-    if (rc != STS_OK) return rc;
-    p.part = ws->part;
-    p.counters = ws->counters;
+  // One workgroup per CU (2-4 per CU measured slower: more partials to
+  // merge, no more bytes in flight per CU).
+  constexpr int chunk_max = 512, chunk_min = 64;
+  const uint64_t target = (uint64_t)device_cu_count();
+  uint64_t want = (target + units - 1) / units;
+  if (want < 1) want = 1;
+  uint64_t c = (max_rows + want - 1) / want;
+  c = (c + unit_rows - 1) / unit_rows * unit_rows;
+  if (c > (uint64_t)chunk_max) c = (uint64_t)chunk_max / unit_rows * unit_rows;
+  if (c < (uint64_t)chunk_min) c = (uint64_t)chunk_min;
+  if (c < unit_rows) c = unit_rows;
+  pl.chunk = (uint32_t)c;
+  pl.nsplit = (max_rows + pl.chunk - 1) / pl.chunk;
+  if (pl.nsplit > (uint32_t)kMaxSplits) {
+    pl.chunk = (max_rows + kMaxSplits - 1) / kMaxSplits;
+    pl.chunk = (pl.chunk + unit_rows - 1) / unit_rows * unit_rows;
+    pl.nsplit = (max_rows + pl.chunk - 1) / pl.chunk;
   }
+  return pl;
+}
+
+int check_decode(const DecodeParams& p, uint32_t batch, uint32_t head_dim) {
+  if (head_dim != 64 && head_dim != 128)
+    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
   if ((uint64_t)p.M * head_dim * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
   if (batch > 65535u || p.H > 65535u)
     return fail(STS_ERR_INVALID, "batch (%u) and heads (%u) must be <= 65535", batch, p.H);
-  const dim3 grid(nsplit, p.H, batch);
+  return STS_OK;
+}
+
+int launch_planned(DecodeParams p, const DecodePlan& pl, uint32_t batch, uint32_t head_dim,
+                   hipStream_t stream) {
+  p.chunk = pl.chunk;
+  p.nsplit_max = pl.nsplit;
+  const dim3 grid(pl.nsplit, p.H, batch);
   if (head_dim == 128) {
-    if (waves == 1)
+    if (pl.waves == 1)
       hipLaunchKernelGGL((decode_kernel<128, 1>), grid, dim3(64), 0, stream, p);
     else
       hipLaunchKernelGGL((decode_kernel<128, 4>), grid, dim3(256), 0, stream, p);
-  } else if (head_dim == 64) {
-    if (waves == 1)
+  } else {
+    if (pl.waves == 1)
       hipLaunchKernelGGL((decode_kernel<64, 1>), grid, dim3(64), 0, stream, p);
     else
       hipLaunchKernelGGL((decode_kernel<64, 4>), grid, dim3(256), 0, stream, p);
-  } else {
-    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
   }
   STS_HIP(hipGetLastError());
   return STS_OK;
+}
+
+// ---- allocation-free variant ------------------------------------------------
+//
+// Split workspace of launch_decode_noalloc, in device memory the code object
+// owns (one copy per GPU, held until the process ends): words
+// [0, kScratchCounters) are the arrival counters (zero between launches, as
+// each launch's last arriver leaves them), the rest the partial records.
+constexpr uint32_t kScratchCounters = 16384;         // 64 KiB
+constexpr uint32_t kScratchPartFloats = 2u << 20;    // 8 MiB
+static __device__ __align__(256) uint32_t scratch[kScratchCounters + kScratchPartFloats];
+
+__global__ void zero_words(uint32_t* p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+std::mutex g_scratch_mutex;
+std::map<int, uint32_t*> g_scratch;  // device -> address of `scratch` on it
+
+// Device address of `scratch` on the current device.  The first call on a
+// device looks it up (the array's name in host code is not a device address)
+// and clears the counters with a fill kernel on `stream`.
+int scratch_address(hipStream_t stream, uint32_t** out) {
+  int dev = 0;
+  STS_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) {
+    *out = it->second;
+    return STS_OK;
+  }
+  uint32_t* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr)
+    return fail(STS_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s (%d)", hipGetErrorString(e),
+                (int)e);
+  hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, stream, ptr, kScratchCounters);
+  STS_HIP(hipGetLastError());
+  g_scratch[dev] = ptr;
+  *out = ptr;
+  return STS_OK;
+}
+
+}  // namespace
+
+int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
+                  hipStream_t stream) {
+  const uint64_t units = (uint64_t)batch * p.H;
+  if (units == 0) return STS_OK;
+  if (int rc = check_decode(p, batch, head_dim)) return rc;
+  const DecodePlan pl = plan_decode(units, max_rows);
+  if (pl.nsplit > 1) {
+    // Partials and arrival counters.
+    Workspace* ws = nullptr;
+    const int rc = get_workspace(stream, (size_t)units * pl.nsplit * (head_dim + 4), units, &ws);
+    if (rc != STS_OK) return rc;
+    p.part = ws->part;
+    p.counters = ws->counters;
+  }
+  return launch_planned(p, pl, batch, head_dim, stream);
+}
+
+int launch_decode_noalloc(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
+                          hipStream_t stream) {
+  const uint64_t units = (uint64_t)batch * p.H;
+  if (units == 0) return STS_OK;
+  if (int rc = check_decode(p, batch, head_dim)) return rc;
+  const DecodePlan pl = plan_decode(units, max_rows);
+  if (pl.nsplit > 1) {
+    const uint64_t need = units * pl.nsplit * (head_dim + 4);
+    if (need > kScratchPartFloats || units > kScratchCounters)
+      return fail(STS_ERR_INVALID,
+                  "this launch needs %llu floats of split records and %llu counters; the "
+                  "static scratch holds %u and %u (use sts_decode_ring)",
+                  (unsigned long long)need, (unsigned long long)units, kScratchPartFloats,
+                  kScratchCounters);
+    uint32_t* ptr = nullptr;
+    if (int rc = scratch_address(stream, &ptr)) return rc;
+    p.counters = ptr;
+    p.part = reinterpret_cast<float*>(ptr + kScratchCounters);
+  }
+  return launch_planned(p, pl, batch, head_dim, stream);
 }
 
 float softmax_scale_log2(float scale) { return scale * kLog2e; }

@@ -45,4 +45,11 @@ float softmax_scale_log2(float scale);
 int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
                   hipStream_t stream);
 
+// launch_decode without allocating: the split records and arrival counters
+// live in a static device array of the library (8 MiB of records, 16384
+// counters per GPU); launches that need more fail with STS_ERR_INVALID.  All
+// calls on one GPU share that array: calls that overlap in time race.
+int launch_decode_noalloc(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
+                          hipStream_t stream);
+
 }  // namespace sts

@@ -64,6 +64,8 @@ SIGNATURES = {
     "sts_fused_attention": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u64, _vp]),
     "sts_cache_write": (_int, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp]),
     "sts_decode_ring": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32, _vp]),
+    "sts_decode_ring_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32,
+                                       _vp]),
     "sts_depformer_step": (_int, [_vp, _vp, _vp, _u64, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                   _u32, _f32, _vp]),
     "sts_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _f32,
