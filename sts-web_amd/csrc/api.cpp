@@ -13,6 +13,7 @@
 #include "append.hpp"
 #include "common.hpp"
 #include "decode.hpp"
+#include "errors.hpp"
 #include "prefill.hpp"
 #include "q4k.hpp"
 
@@ -602,7 +603,7 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
 int sts_device_errors(void* stream, uint32_t* flags) {
   sts::clear_error();
   uint32_t f = 0;
-  if (int rc = sts::take_prefill_errors(as_stream(stream), &f)) return rc;
+  if (int rc = sts::take_device_errors(as_stream(stream), &f)) return rc;
   if (flags) *flags = f;
   if (f & STS_DEVERR_WAIT_TIMEOUT)
     return fail(STS_ERR_DEVICE,

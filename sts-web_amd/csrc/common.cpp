@@ -2,6 +2,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -54,12 +55,12 @@ int get_workspace(hipStream_t stream, size_t part_floats, size_t n_counters, Wor
     // The old buffers are retired, not freed: kernels queued on the stream
     // and graphs captured earlier keep using them.  Growth at least doubles,
     // so the retired buffers never exceed the live ones.
-    size_t pf = std::max(part_floats, 2 * ws.part_floats);
-    size_t nc = std::max(n_counters, 2 * ws.n_counters);
-    pf = std::max<size_t>(pf, 1);
-    nc = std::max<size_t>(nc, 1);
-    pf = (pf + 65535) & ~size_t(65535);
-    nc = (nc + 1023) & ~size_t(1023);
+    auto grow = [](size_t want, size_t have, size_t round) {
+      const size_t n = std::max<size_t>(std::max(want, have < want ? 2 * have : have), 1);
+      return (n + round - 1) / round * round;
+    };
+    const size_t pf = grow(part_floats, ws.part_floats, 65536);
+    const size_t nc = grow(n_counters, ws.n_counters, 1024);
     float* part = nullptr;
     uint32_t* counters = nullptr;
     if (hipMalloc(&part, pf * sizeof(float)) != hipSuccess)
@@ -84,6 +85,13 @@ int get_workspace(hipStream_t stream, size_t part_floats, size_t n_counters, Wor
   *out = &ws;
   return STS_OK;
 }
+
+namespace {
+std::atomic<uint32_t> g_wait_limit{1u << 24};
+}  // namespace
+
+void set_wait_limit(uint32_t polls) { g_wait_limit = polls ? polls : (1u << 24); }
+uint32_t wait_limit() { return g_wait_limit; }
 
 int device_cu_count() {
   int dev = 0;

@@ -50,4 +50,8 @@ int get_workspace(hipStream_t stream, size_t part_floats, size_t n_counters, Wor
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Poll bound of the kernels' bounded waits (0 restores the default, 2^24).
+void set_wait_limit(uint32_t polls);
+uint32_t wait_limit();
+
 }  // namespace sts

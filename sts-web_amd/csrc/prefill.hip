@@ -27,13 +27,11 @@
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
 // L2 copy of the head's K/V; the heaviest (last) q-tiles are dispatched first.
 #include <algorithm>
-#include <atomic>
 #include <cfloat>
-#include <map>
-#include <mutex>
 
 #include "coherent.hpp"
 #include "common.hpp"
+#include "errors.hpp"
 #include "lane.hpp"
 #include "prefill.hpp"
 #include "rope.hpp"
@@ -48,15 +46,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;  // queries per workgroup
 constexpr int kBK = 64;  // keys per LDS block
-
-// Error bits (STS_DEVERR_*) raised by the kernels of this file on the current
-// device, and the word take_errors_kernel moves them to for the host.
-__device__ uint32_t g_prefill_errors;
-__device__ uint32_t g_prefill_errors_taken;
-
-__global__ void take_errors_kernel() {
-  if (threadIdx.x == 0) g_prefill_errors_taken = atomicExch(&g_prefill_errors, 0u);
-}
 
 // Query row of q (scaled by zero when the lane has no query) with optional
 // RoPE at table row rope_pos0 + i: four dims d0..d0+3.
@@ -552,13 +541,13 @@ constexpr int kWaitLgkm0 = 0xC07F;
 // in the device error word (the stage it goes on with may not hold its block,
 // so the output is wrong, and the host learns it from that word).
 __device__ __forceinline__ void ws_wait_ge(const uint32_t* ctr, uint32_t target, uint32_t limit,
-                                           int lane) {
+                                           int lane, uint32_t* err) {
   bool done = false;
   for (uint32_t spin = 0; spin < limit && !done; ++spin) {
     done = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target;
     if (!done) __builtin_amdgcn_s_sleep(1);
   }
-  if (!done && lane == 0) atomicOr(&g_prefill_errors, (uint32_t)STS_DEVERR_WAIT_TIMEOUT);
+  if (!done && lane == 0 && err) atomicOr(err, (uint32_t)STS_DEVERR_WAIT_TIMEOUT);
   asm volatile("" ::: "memory");
 }
 // Publishes this wave's LDS writes (or the end of its LDS reads) and counts it.
@@ -728,7 +717,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // stage's previous block (4 releases per use).
     auto produce = [&](const Buf& bf, uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
-      ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane);
+      ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane, p.err);
       put(bf, st[s]);
       ws_signal(&filled[s], lane);
     };
@@ -809,14 +798,14 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         }
       }
     } else {
-      ws_wait_ge(&q_ready, 4, p.wait_limit, lane);
+      ws_wait_ge(&q_ready, 4, p.wait_limit, lane, p.err);
 #pragma unroll
       for (int a = 0; a < KA; ++a)
         qop[0][a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
     }
     for (uint32_t i = 0; i < nblk; ++i) {
       const uint32_t s = i % NS, use = i / NS;
-      ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane);
+      ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane, p.err);
       const Stage& sg = st[s];
       const uint32_t k0 = i * KB + ks * 32;
       f32x16 sc;
@@ -981,40 +970,6 @@ int launch_f32(const PrefillParams& p, hipStream_t stream) {
 
 }  // namespace
 
-namespace {
-std::atomic<uint32_t> g_wait_limit{1u << 24};
-std::mutex g_err_mutex;
-std::map<int, uint32_t*> g_err_taken;  // per device: address of g_prefill_errors_taken
-}  // namespace
-
-void set_wait_limit(uint32_t polls) { g_wait_limit = polls ? polls : (1u << 24); }
-uint32_t wait_limit() { return g_wait_limit; }
-
-int take_prefill_errors(hipStream_t stream, uint32_t* flags) {
-  int dev = 0;
-  STS_HIP(hipGetDevice(&dev));
-  uint32_t* taken = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_err_mutex);
-    auto it = g_err_taken.find(dev);
-    if (it != g_err_taken.end()) {
-      taken = it->second;
-    } else {
-      STS_HIP(hipGetSymbolAddress(reinterpret_cast<void**>(&taken),
-                                  HIP_SYMBOL(g_prefill_errors_taken)));
-      g_err_taken[dev] = taken;
-    }
-  }
-  // The word is swapped to zero on the device (no flag raised between the
-  // read and the clear is lost), after the work queued on `stream`.
-  hipLaunchKernelGGL(take_errors_kernel, dim3(1), dim3(64), 0, stream);
-  STS_HIP(hipGetLastError());
-  STS_HIP(hipStreamSynchronize(stream));
-  uint32_t v = 0;
-  STS_HIP(hipMemcpy(&v, taken, sizeof v, hipMemcpyDeviceToHost));
-  *flags = v;
-  return STS_OK;
-}
 
 int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_len,
                   int precision) {
@@ -1033,7 +988,8 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
 int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hipStream_t stream) {
   if (int rc = check_prefill(p0.S, p0.H, head_dim, p0.M, precision)) return rc;
   PrefillParams p = p0;
-  p.wait_limit = g_wait_limit;
+  p.wait_limit = wait_limit();
+  if (int rc = device_error_word(&p.err)) return rc;
   const bool d128 = head_dim == 128;
   switch (precision) {
     case STS_PREC_BF16_MFMA:

@@ -32,6 +32,7 @@ struct PrefillParams {
   // Polls after which a bounded wait of the bf16 kernels gives up and records
   // STS_DEVERR_WAIT_TIMEOUT in the device error word.
   uint32_t wait_limit = 1u << 24;
+  uint32_t* err = nullptr;  // the device error word
 };
 
 // Checks everything launch_prefill would reject for these sizes, without
@@ -41,12 +42,5 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
 
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream);
 
-// Poll bound given to the bf16 kernels' waits (0 restores the default).
-void set_wait_limit(uint32_t polls);
-uint32_t wait_limit();
-
-// Reads and clears the prefill kernels' device error word on the current
-// device (after synchronising `stream`); *flags gets the STS_DEVERR_* bits.
-int take_prefill_errors(hipStream_t stream, uint32_t* flags);
 
 }  // namespace sts

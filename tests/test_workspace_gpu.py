@@ -154,3 +154,4 @@ def test_bounded_wait_give_up_is_reported(gpu, prec):
     ref = oracle.prefill_f64(q, kc, vc, start, L, scale_for(D))
     tol = 2e-2 if prec == sts_attn.PREC_BF16_MFMA else 1e-4
     assert np.abs(got - ref).max() < tol
+
