@@ -286,7 +286,7 @@ def bench_q4k(torch, sts, stream, steps, warmup):
            "weight_bytes_per_frame": w_bytes,
            "gbs": (w_bytes + io_bytes) / (us * 1e-6) / 1e9}
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
-    res["_layer0"] = layers[0]
+    res["_layers"] = layers
     for name, (n, k) in (("linear_in", (22528, K)), ("linear_out", (K, 11264))):
         ws = [sts.Q4KTensor(q4k_random(torch, g, n, k), (n, k)) for _ in range(4)]
         xi = torch.randn((1, 1, k), generator=g, device="cuda")
@@ -392,75 +392,133 @@ def bench_depformer_frame(torch, sts, stream, steps, warmup):
     return res
 
 
+def cpu_info():
+    """The host's CPU as this process sees it: model string, nproc, the CPUs the
+    process may run on, and the threads the baseline uses -- all it may use,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box gives
+    one GPU's jobs a 16-core share and sets OMP_NUM_THREADS to that)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = nproc
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(allowed, int(env)) if env.isdigit() and int(env) > 0 else allowed
+    return {"cpu_model": model, "nproc": nproc, "affinity": allowed, "threads": threads,
+            "omp_num_threads_env": env or None}
+
+
+def _median_time(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(sorted(ts)[len(ts) // 2])
+
+
 def cpu_baseline_depformer_frame(torch, cfg, w, args):
     """The oracle's restatement of the chain (every op in its shader's f32
-    order) for stream 0 of the benchmarked frame, scaled to the 64 streams."""
+    order, OpenMP inside each op) for the benchmarked frame: all 64 streams on
+    the allowed threads; one thread on stream 0, scaled to 64 streams."""
     import numpy as np
     sys.path.insert(0, ROOT)
     import oracle
-    cores = min(os.cpu_count() or 1, 16)
-    oracle.set_num_threads(cores)
+    info = cpu_info()
     c = {f: getattr(cfg, f) for f, _ in cfg._fields_}
     host = {f: [t.cpu().numpy() for t in w[f]] for f in oracle.DepformerWeights.FIELDS}
     ow = oracle.DepformerWeights(c, text_emb=w["text_emb"].cpu().numpy(), **host)
     th, text, temp, top_k, pen, rand, pt, npn = args
-    t0 = time.perf_counter()
-    oracle.depformer_generate(ow, th[0].cpu().numpy(), int(text[0]), top_k, temp, pen,
-                              rand[0].cpu().numpy(), pt[0].cpu().numpy().view(np.uint32),
-                              npn[0].cpu().numpy().view(np.uint32))
-    us = (time.perf_counter() - t0) * 1e6
-    return {"value": us * DEPF_STREAMS, "unit": "us/frame", "cores": cores, "kind": "port",
-            "sample": f"stream 0 of the frame (1 run), oracle shader-order f32 chain, "
-                      f"OpenMP inside each op, scaled x{DEPF_STREAMS}"}
+    th, text, rand = th.cpu().numpy(), text.cpu().numpy(), rand.cpu().numpy()
+    pt, npn = pt.cpu().numpy().view(np.uint32), npn.cpu().numpy().view(np.uint32)
+
+    def stream(b):
+        oracle.depformer_generate(ow, th[b], int(text[b]), top_k, temp, pen, rand[b], pt[b],
+                                  npn[b])
+    oracle.set_num_threads(info["threads"])
+    stream(0)
+    us = _median_time(lambda: [stream(b) for b in range(DEPF_STREAMS)], 1) * 1e6
+    oracle.set_num_threads(1)
+    us1 = _median_time(lambda: stream(0), 1) * 1e6 * DEPF_STREAMS
+    oracle.set_num_threads(info["threads"])
+    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
+            "one_thread_us": us1, **info,
+            "sample": f"all {DEPF_STREAMS} streams of the benchmarked frame, one after another "
+                      f"(OpenMP inside each op); the 1-thread figure runs stream 0 and scales "
+                      f"x{DEPF_STREAMS}"}
 
 
-def cpu_baseline_q4k(torch, layer):
-    """The oracle's restatement of shader_q4k_matvec.wgsl on this host's cores:
-    layer 0's in_proj and out_proj (x0 of one frame), scaled to 24 layers."""
+def cpu_baseline_q4k(torch, layers):
+    """The oracle's restatement of shader_q4k_matvec.wgsl (OpenMP over output
+    rows): the whole frame, in_proj + out_proj of all 24 layers, on the allowed
+    threads (median of 3) and on one thread."""
     import numpy as np
     sys.path.insert(0, ROOT)
     import oracle
-    cores = min(os.cpu_count() or 1, 16)
-    oracle.set_num_threads(cores)
+    info = cpu_info()
     x = np.ascontiguousarray(np.random.default_rng(0).standard_normal((1, 4096)), np.float32)
-    wi, wo = (w.raw.cpu().numpy() for w in layer)
-    t0 = time.perf_counter()
-    for _ in range(2):
-        oracle.q4k_matvec_wgsl(wi, x, 3 * 4096)
-        oracle.q4k_matvec_wgsl(wo, x, 4096)
-    us_layer = (time.perf_counter() - t0) / 2 * 1e6
-    return {"value": us_layer * LAYERS, "unit": "us/frame", "cores": cores, "kind": "port",
-            "sample": "layer 0 in_proj + out_proj (2 runs), oracle shader-order f32 Q4_K "
-                      f"matvec, OpenMP over rows, scaled x{LAYERS}"}
+    ws = [(wi.raw.cpu().numpy(), wo.raw.cpu().numpy()) for wi, wo in layers]
+
+    def frame():
+        for wi, wo in ws:
+            oracle.q4k_matvec_wgsl(wi, x, 3 * 4096)
+            oracle.q4k_matvec_wgsl(wo, x, 4096)
+    oracle.set_num_threads(info["threads"])
+    frame()
+    us = _median_time(frame, 3) * 1e6
+    oracle.set_num_threads(1)
+    us1 = _median_time(frame, 1) * 1e6
+    oracle.set_num_threads(info["threads"])
+    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
+            "one_thread_us": us1, **info,
+            "sample": f"the whole frame: in_proj + out_proj of all {LAYERS} layers (x0 of one "
+                      f"frame), oracle shader-order f32 Q4_K matvec"}
 
 
 def cpu_baseline(torch, dec):
-    """The oracle's restatement of shader_attention.wgsl, on this host's cores,
-    over 2 of the 24 layers of the decode workload, scaled to us/frame."""
+    """The oracle's restatement of shader_attention.wgsl (f32, the shader's lane
+    and tree order), for the whole benchmarked decode frame: 24 layers x 32
+    heads x 3000 rows, parallel over (layer, head) on the allowed threads
+    (median of 5 after a warm-up) and on one thread (median of 3)."""
     import numpy as np
     sys.path.insert(0, ROOT)
     import oracle
-    cores = min(os.cpu_count() or 1, 16)
-    oracle.set_num_threads(cores)
-    n_layers = 2
+    info = cpu_info()
     scale = float(np.float32(D) ** np.float32(-0.5))
-    times = []
-    for layer in range(n_layers):
+    qs, kcs, vcs, starts, lens = [], [], [], [], []
+    for layer in range(LAYERS):
         c = dec["caches"][layer]
         kb, vb = c.read_buffers()
-        start, ln = c.window()
-        kc = kb[0].cpu().numpy()
-        vc = vb[0].cpu().numpy()
-        qh = dec["q"][layer, 0].cpu().numpy()
-        t0 = time.perf_counter()
-        for _ in range(3):
-            oracle.attention_ring_wgsl(qh, kc, vc, start, ln, scale)
-        times.append((time.perf_counter() - t0) / 3)
-    us_layer = float(np.median(times)) * 1e6
-    return {"value": us_layer * LAYERS, "unit": "us/frame", "cores": cores, "kind": "port",
-            "sample": f"{n_layers} of {LAYERS} layers (32 heads x 3000 rows each, 3 runs), "
-                      f"oracle shader-order f32 attention, OpenMP over heads, scaled x{LAYERS}",
-            "us_per_layer": us_layer}
+        st, ln = c.window()
+        kcs.append(np.ascontiguousarray(kb[0].cpu().numpy()))
+        vcs.append(np.ascontiguousarray(vb[0].cpu().numpy()))
+        qs.append(np.ascontiguousarray(dec["q"][layer, 0].cpu().numpy()))
+        starts.append(st)
+        lens.append(ln)
+        del kb, vb
+
+    def frame():
+        oracle.decode_frame_wgsl(qs, kcs, vcs, starts, lens, scale)
+    oracle.set_num_threads(info["threads"])
+    frame()
+    us = _median_time(frame, 5) * 1e6
+    oracle.set_num_threads(1)
+    us1 = _median_time(frame, 3) * 1e6
+    oracle.set_num_threads(info["threads"])
+    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
+            "one_thread_us": us1, **info,
+            "sample": f"the whole frame: {LAYERS} layers x {H} heads x {M} rows (the benchmarked "
+                      f"caches and queries, attention only), oracle shader-order f32 attention, "
+                      f"OpenMP over (layer, head)"}
 
 
 def load_traffic():
@@ -573,12 +631,12 @@ def main():
         line["ragged"]["frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     if "q4k" in extra:
         q = extra["q4k"]
-        layer0 = q.pop("_layer0")
+        layers_all = q.pop("_layers")
         line["q4k_projections"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                    for k, v in q.items()}
         if not args.no_cpu:
             log("bench: cpu baseline (q4k)")
-            cq = cpu_baseline_q4k(torch, layer0)
+            cq = cpu_baseline_q4k(torch, layers_all)
             line["q4k_projections"]["cpu_baseline"] = cq
             line["q4k_projections"]["gpu_vs_cpu"] = round(cq["value"] / q["us_per_frame"], 1)
     if "depformer_frame" in extra:

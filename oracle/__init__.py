@@ -67,6 +67,10 @@ def _load():
                                       ctypes.c_float, _u64]),
         "orc_attention_ring_wgsl": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32,
                                            _u32, _u32, ctypes.c_float]),
+        "orc_decode_frame_wgsl": (None, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p, _u32, _u32, _u32, _u32,
+                                         ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                                         ctypes.c_float]),
         "orc_attention_ring_f64": (None, [_f32p, _f32p, _f32p, _f64p, _u32, _u32, _u32,
                                           _u32, _u32, ctypes.c_double]),
         "orc_prefill_f64": (None, [_f32p, _f32p, _f32p, _f64p, _u32, _u32, _u32, _u32,
@@ -226,6 +230,24 @@ def attention_ring_wgsl(q, kc, vc, start: int, length: int, scale: float) -> np.
                                   _p32(np.ascontiguousarray(vc)), _p32(out), H, D, M, start,
                                   length, scale)
     return out
+
+
+def decode_frame_wgsl(qs, kcs, vcs, starts, lens, scale: float) -> list:
+    """Shader-order decode of every (layer, head), parallel over (layer, head):
+    qs[l] [H,D], kcs[l]/vcs[l] [H,M,D], window of layer l = lens[l] rows from
+    slot starts[l].  Returns the outputs [H,D] per layer.  The arrays are used
+    in place (they must be C-contiguous float32)."""
+    L = len(qs)
+    H, M, D = kcs[0].shape
+    for a in list(qs) + list(kcs) + list(vcs):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    outs = [np.empty((H, D), np.float32) for _ in range(L)]
+    arr = lambda xs: (ctypes.c_void_p * L)(*[x.ctypes.data for x in xs])
+    st = (_u32 * L)(*[int(x) for x in starts])
+    ln = (_u32 * L)(*[int(x) for x in lens])
+    lib().orc_decode_frame_wgsl(arr(qs), arr(kcs), arr(vcs), arr(outs), L, H, D, M, st, ln,
+                                scale)
+    return outs
 
 
 def attention_ring_f64(q, kc, vc, start: int, length: int, scale: float) -> np.ndarray:

@@ -17,6 +17,16 @@
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
+
+/* Hot loops are compiled for several x86-64 levels and dispatched at load time
+ * by the CPU's features (the library is built here and runs on another host's
+ * CPU).  The floating-point order does not depend on the level: every f32
+ * product and sum is rounded separately (-ffp-contract=off, no fast-math). */
+#if defined(__x86_64__)
+#define ORC_MULTIARCH __attribute__((target_clones("avx512f", "avx2", "default")))
+#else
+#define ORC_MULTIARCH
+#endif
 #endif
 
 /* ------------------------------------------------------------------------ */
@@ -160,38 +170,68 @@ void orc_kv_rollback(orc_kv* c, uint64_t n) {    /* model.rs:352-362 */
 
 #define WG 256u /* shader_attention.wgsl:35 */
 
+/* Interleave width of phase 1: ILANES lanes' rows are processed together so
+ * that their dot products (each a sequential sum over d, as the shader's) run
+ * as independent dependency chains.  Every lane's arithmetic is performed in
+ * exactly the shader's order; only lanes are interleaved. */
+#define ILANES 8u
+
+/* Row `pos` of a head's window: rows are contiguous (ring == 0) or live in
+ * slot (start + pos) % M of a ring of M rows. */
+static inline const float* win_row(const float* h, uint32_t D, uint32_t ring, uint32_t start,
+                                   uint32_t pos) {
+  const uint32_t slot = ring ? (uint32_t)(((uint64_t)start + pos) % ring) : pos;
+  return h + (size_t)slot * D;
+}
+
+ORC_MULTIARCH
 static void attention_wgsl_head(const float* q_reg, const float* kh, const float* vh,
                                 float* out, uint32_t D, uint32_t S, float scale,
+                                uint32_t ring, uint32_t start,
                                 float* p_v /* [WG][D] */, float* p_max, float* p_sum,
                                 float* sh_max, float* sh_sum, float* sh_v) {
   /* Phase 1 (:64-101): per-lane online softmax over rows tid, tid+WG, ... */
-  for (uint32_t tid = 0; tid < WG; ++tid) {
-    float m = -3.402823e+38f;                                     /* :71 */
-    float l = 0.0f;                                               /* :72 */
-    float* pv = p_v + (size_t)tid * D;
-    for (uint32_t d = 0; d < D; ++d) pv[d] = 0.0f;                /* :74-76 */
-    for (uint32_t pos = tid; pos < S; pos += WG) {                /* :78-100 */
-      float dot = 0.0f;
-      const float* kr = kh + (size_t)pos * D;
-      for (uint32_t d = 0; d < D; ++d) {
-        const float prod = q_reg[d] * kr[d];
-        dot = dot + prod;                                         /* :82-84 */
+  for (uint32_t t0 = 0; t0 < WG; t0 += ILANES) {
+    float m[ILANES], l[ILANES];
+    for (uint32_t j = 0; j < ILANES; ++j) {
+      m[j] = -3.402823e+38f;                                      /* :71 */
+      l[j] = 0.0f;                                                /* :72 */
+      float* pv = p_v + (size_t)(t0 + j) * D;
+      for (uint32_t d = 0; d < D; ++d) pv[d] = 0.0f;              /* :74-76 */
+    }
+    for (uint32_t base = t0; base < S; base += WG) {              /* :78-100 */
+      const uint32_t n = S - base < ILANES ? S - base : ILANES;   /* lanes with a row */
+      const float* kr[ILANES];
+      float dot[ILANES];
+      for (uint32_t j = 0; j < ILANES; ++j) {
+        kr[j] = win_row(kh, D, ring, start, j < n ? base + j : base);
+        dot[j] = 0.0f;
       }
-      dot = dot * scale;                                          /* :85 */
-      const float old_max = m;
-      m = fmaxf(m, dot);                                          /* :88 */
-      const float alpha = expf(old_max - m);                      /* :89 */
-      const float w = expf(dot - m);                              /* :90 */
-      l = l * alpha + w;                                          /* :92 */
-      const float* vr = vh + (size_t)pos * D;
-      for (uint32_t d = 0; d < D; ++d) {
-        const float a = pv[d] * alpha;
-        const float b = w * vr[d];
-        pv[d] = a + b;                                            /* :95-97 */
+      for (uint32_t d = 0; d < D; ++d)
+        for (uint32_t j = 0; j < ILANES; ++j) {
+          const float prod = q_reg[d] * kr[j][d];
+          dot[j] = dot[j] + prod;                                 /* :82-84 */
+        }
+      for (uint32_t j = 0; j < n; ++j) {
+        const float sc = dot[j] * scale;                          /* :85 */
+        const float old_max = m[j];
+        m[j] = fmaxf(m[j], sc);                                   /* :88 */
+        const float alpha = expf(old_max - m[j]);                 /* :89 */
+        const float w = expf(sc - m[j]);                          /* :90 */
+        l[j] = l[j] * alpha + w;                                  /* :92 */
+        const float* vr = win_row(vh, D, ring, start, base + j);
+        float* pv = p_v + (size_t)(t0 + j) * D;
+        for (uint32_t d = 0; d < D; ++d) {
+          const float a = pv[d] * alpha;
+          const float b = w * vr[d];
+          pv[d] = a + b;                                          /* :95-97 */
+        }
       }
     }
-    p_max[tid] = m;
-    p_sum[tid] = l;
+    for (uint32_t j = 0; j < ILANES; ++j) {
+      p_max[t0 + j] = m[j];
+      p_sum[t0 + j] = l[j];
+    }
   }
   /* Phase 2 (:106-124): tree merge of (max, sum). */
   for (uint32_t t = 0; t < WG; ++t) {
@@ -239,8 +279,8 @@ void orc_attention_wgsl(const float* q, const float* k, const float* v, float* o
     for (int64_t hh = 0; hh < (int64_t)H; ++hh) {
       const uint32_t h = (uint32_t)hh;
       attention_wgsl_head(q + (size_t)h * D, k + (size_t)h * kv_head_stride,
-                          v + (size_t)h * kv_head_stride, out + (size_t)h * D, D, S, scale,
-                          p_v, scratch, scratch + WG, scratch + 2 * WG, scratch + 3 * WG,
+                          v + (size_t)h * kv_head_stride, out + (size_t)h * D, D, S, scale, 0,
+                          0, p_v, scratch, scratch + WG, scratch + 2 * WG, scratch + 3 * WG,
                           scratch + 4 * WG);
     }
     free(p_v);
@@ -270,6 +310,32 @@ void orc_attention_ring_wgsl(const float* q, const float* kc, const float* vc, f
   orc_attention_wgsl(q, kg, vg, out, H, D, len, scale, (uint64_t)len * D);
   free(kg);
   free(vg);
+}
+
+/* A temporal decode frame on the CPU: decode attention of every (layer, head)
+ * over its ring window, in the shader's order, parallel over (layer, head) --
+ * the CPU path a host without WebGPU would run for shader_attention.wgsl.
+ * q[l], out[l]: [H][D]; kc[l], vc[l]: [H][M][D]; window of layer l: rows
+ * 0..lens[l]-1 in slots (starts[l] + i) % M. */
+void orc_decode_frame_wgsl(const float* const* q, const float* const* kc,
+                           const float* const* vc, float* const* out, uint32_t L, uint32_t H,
+                           uint32_t D, uint32_t M, const uint32_t* starts, const uint32_t* lens,
+                           float scale) {
+#pragma omp parallel
+  {
+    float* p_v = (float*)malloc(sizeof(float) * WG * D);
+    float* scratch = (float*)malloc(sizeof(float) * WG * 5);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t t = 0; t < (int64_t)L * H; ++t) {
+      const uint32_t l = (uint32_t)(t / H), h = (uint32_t)(t % H);
+      attention_wgsl_head(q[l] + (size_t)h * D, kc[l] + (size_t)h * M * D,
+                          vc[l] + (size_t)h * M * D, out[l] + (size_t)h * D, D, lens[l], scale, M,
+                          starts[l] % M, p_v, scratch, scratch + WG, scratch + 2 * WG,
+                          scratch + 3 * WG, scratch + 4 * WG);
+    }
+    free(p_v);
+    free(scratch);
+  }
 }
 
 /* ------------------------------------------------------------------------ */

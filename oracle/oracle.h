@@ -84,6 +84,12 @@ void orc_attention_wgsl(const float* q, const float* k, const float* v, float* o
 void orc_attention_ring_wgsl(const float* q, const float* kc, const float* vc, float* out,
                              uint32_t H, uint32_t D, uint32_t M, uint32_t start,
                              uint32_t len, float scale);
+/* A temporal decode frame: every (layer, head) over its ring window, shader
+ * order, parallel over (layer, head). */
+void orc_decode_frame_wgsl(const float* const* q, const float* const* kc,
+                           const float* const* vc, float* const* out, uint32_t L, uint32_t H,
+                           uint32_t D, uint32_t M, const uint32_t* starts, const uint32_t* lens,
+                           float scale);
 
 /*
  * Textbook softmax(scale * q K^T) V in double over the same ring window

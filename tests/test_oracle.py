@@ -405,3 +405,22 @@ def test_golden_input_hash_is_stable():
     h = hashlib.sha256(oracle.normal(101, (1, 1, 32, 128)).tobytes()).hexdigest()
     h2 = hashlib.sha256(oracle.normal(101, (1, 1, 32, 128)).tobytes()).hexdigest()
     assert h == h2
+
+
+def test_decode_frame_equals_per_layer_shader_order():
+    """orc_decode_frame_wgsl (the bench's CPU baseline: every (layer, head) in
+    parallel, rows read in their ring slots) equals attention_ring_wgsl layer by
+    layer, bit for bit, including a window shorter than the ring and one that
+    wraps."""
+    H, D, M = 3, 64, 300
+    qs, kcs, vcs = [], [], []
+    starts, lens = [0, 250, 17], [300, 300, 41]
+    for layer in range(3):
+        qs.append(oracle.normal(10 + layer, (H, D)))
+        kcs.append(oracle.normal(20 + layer, (H, M, D)))
+        vcs.append(oracle.normal(30 + layer, (H, M, D)))
+    got = oracle.decode_frame_wgsl(qs, kcs, vcs, starts, lens, 0.125)
+    for layer in range(3):
+        want = oracle.attention_ring_wgsl(qs[layer], kcs[layer], vcs[layer], starts[layer],
+                                          lens[layer], 0.125)
+        np.testing.assert_array_equal(got[layer], want)
