@@ -157,6 +157,29 @@ def bench_prefill(torch, sts, stream, steps, warmup):
         us_layer = t.ms * 1e3 / steps / LAYERS
         res[name] = {"us_per_layer": us_layer,
                      "tflops": flops_layer / (us_layer * 1e-6) / 1e12}
+    # bf16-MFMA over a bf16 mirror of the caches (what a KV handle created with
+    # STS_KV_BF16_MIRROR keeps): same result as "bf16" bit for bit, half the
+    # K/V bytes.
+    k16 = kc.to(torch.bfloat16)
+    v16 = vc.to(torch.bfloat16)
+
+    def run16():
+        for layer in range(LAYERS):
+            sts.prefill_attention_bf16kv(q[layer], k16[layer], v16[layer], starts[layer], L, scale,
+                                         out=out[layer], stream=stream)
+    for _ in range(warmup):
+        run16()
+    with Timer(torch, stream) as t:
+        for _ in range(steps):
+            run16()
+    us_layer = t.ms * 1e3 / steps / LAYERS
+    res["bf16kv"] = {"us_per_layer": us_layer,
+                     "tflops": flops_layer / (us_layer * 1e-6) / 1e12}
+    # Algorithmic HBM bytes per layer: K/V rows of the window (f32, or bf16
+    # for the mirror), Q read and O written (f32).
+    qo = 2 * S * H * D * 4
+    res["bytes_f32kv"] = 2 * L * H * D * 4 + qo
+    res["bytes_bf16kv"] = 2 * L * H * D * 2 + qo
     return res
 
 
@@ -622,7 +645,14 @@ def main():
             # products per f32 product: priced against the bf16 peak at three products per flop.
             "f32split_us_per_layer": round(p["f32split"]["us_per_layer"], 3),
             "f32split_tflops": round(p["f32split"]["tflops"], 1),
-            "f32split_frac_of_mfma_peak": round(3 * p["f32split"]["tflops"] / BF16_PEAK_TFLOPS, 4)}
+            "f32split_frac_of_mfma_peak": round(3 * p["f32split"]["tflops"] / BF16_PEAK_TFLOPS, 4),
+            # HBM roof of each variant: its algorithmic bytes at 8 TB/s.
+            "bf16_frac_of_hbm_roof": round(p["bytes_f32kv"] / (HBM_PEAK_GBS * 1e3)
+                                           / p["bf16"]["us_per_layer"], 4),
+            "bf16kv_us_per_layer": round(p["bf16kv"]["us_per_layer"], 3),
+            "bf16kv_tflops": round(p["bf16kv"]["tflops"], 1),
+            "bf16kv_frac_of_hbm_roof": round(p["bytes_bf16kv"] / (HBM_PEAK_GBS * 1e3)
+                                             / p["bf16kv"]["us_per_layer"], 4)}
     if "depformer" in extra:
         line["depformer"] = {k: round(v, 3) for k, v in extra["depformer"].items()}
     if "ragged" in extra:

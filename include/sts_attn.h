@@ -191,6 +191,20 @@ int sts_prefill_attention(const float* q, const float* k_cache, const float* v_c
                           uint32_t max_len, uint32_t win_start, uint32_t win_len,
                           float scale, int precision, void* stream);
 
+/*
+ * sts_prefill_attention at STS_PREC_BF16_MFMA over bf16 copies of the caches:
+ * k16, v16 [heads][max_len][head_dim] hold the caches' values rounded to bf16
+ * (nearest even, the rounding that precision applies to the f32 rows), so
+ * the result equals sts_prefill_attention's bit for bit while the kernel
+ * reads half the K/V bytes and converts nothing.  No counterpart in the
+ * reference; the bf16 mirror of a KV handle (STS_KV_BF16_MIRROR) keeps such
+ * copies.  All pointers 16-byte aligned.
+ */
+int sts_prefill_attention_bf16kv(const float* q, const uint16_t* k16, const uint16_t* v16,
+                                 float* out, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                                 uint32_t max_len, uint32_t win_start, uint32_t win_len,
+                                 float scale, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* RoPE (model.rs:38-122)                                                     */
 /* ------------------------------------------------------------------------ */
@@ -232,11 +246,37 @@ typedef struct sts_kv_state {
   uint64_t head_dim;
   uint64_t batch;     /* 0 until the buffers are allocated                 */
   int32_t allocated;  /* 1 when the K/V buffers exist                      */
-  int32_t reserved;
+  int32_t flags;      /* the sts_kv_create_ex flags (STS_KV_BF16_MIRROR)   */
 } sts_kv_state;
+
+/* sts_kv_create_ex flag: keep a bf16 copy of K and V (see sts_kv_create_ex). */
+#define STS_KV_BF16_MIRROR 1u
 
 /* KVCache::new (model.rs:207-219).  Allocates nothing on the device. */
 int sts_kv_create(uint64_t max_len, uint64_t heads, uint64_t head_dim, sts_kv_cache** out);
+
+/*
+ * sts_kv_create with flags; no counterpart in the reference (its caches are
+ * f32 only).  STS_KV_BF16_MIRROR: the handle also keeps K and V rounded to
+ * bf16 (nearest even; same layout, half the bytes), written by every append
+ * made through the handle (sts_kv_update, sts_kv_decode_step,
+ * sts_kv_prefill) and cleared with the caches.  sts_kv_prefill with
+ * STS_PREC_BF16_MFMA then reads the mirror: the same result bit for bit (it
+ * holds exactly the values that kernel rounds the f32 rows to), half the K/V
+ * bytes.  The f32 caches stay the reference's, bit for bit.  Rows written
+ * into the f32 buffers by other means (sts_cache_write on the pointers of
+ * sts_kv_ensure_allocated) reach the mirror only through sts_kv_sync_mirror.
+ * A mirrored cache needs 16-byte aligned inputs in sts_kv_update.
+ */
+int sts_kv_create_ex(uint64_t max_len, uint64_t heads, uint64_t head_dim, uint32_t flags,
+                     sts_kv_cache** out);
+
+/* The bf16 mirror buffers [batch][heads][max_len][head_dim] (bf16 bits), or
+ * NULL when the cache has none or is not allocated yet. */
+int sts_kv_mirror(const sts_kv_cache* cache, uint16_t** k16, uint16_t** v16);
+
+/* Rebuilds the bf16 mirror from the f32 caches (after direct writes). */
+int sts_kv_sync_mirror(sts_kv_cache* cache, void* stream);
 int sts_kv_destroy(sts_kv_cache* cache);
 
 /*

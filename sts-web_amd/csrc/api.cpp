@@ -30,8 +30,11 @@ struct sts_kv_cache {
   uint64_t max_len = 0, heads = 0, head_dim = 0;
   uint64_t offset = 0, len = 0, write_pos = 0;
   uint64_t batch = 0;
+  uint32_t flags = 0;
   float* k = nullptr;
   float* v = nullptr;
+  uint16_t* k16 = nullptr;  // bf16 mirror (STS_KV_BF16_MIRROR)
+  uint16_t* v16 = nullptr;
 };
 
 namespace {
@@ -86,11 +89,31 @@ int kv_ensure(sts_kv_cache* c, uint64_t batch, hipStream_t stream) {
     return fail(STS_ERR_NOMEM, "V cache allocation of %llu bytes failed",
                 (unsigned long long)(n * sizeof(float)));
   }
+  if (c->flags & STS_KV_BF16_MIRROR) {
+    if (hipMalloc(&c->k16, n * sizeof(uint16_t)) != hipSuccess ||
+        hipMalloc(&c->v16, n * sizeof(uint16_t)) != hipSuccess) {
+      for (void* ptr : {(void*)c->k, (void*)c->v, (void*)c->k16, (void*)c->v16})
+        if (ptr) (void)hipFree(ptr);
+      c->k = c->v = nullptr;
+      c->k16 = c->v16 = nullptr;
+      return fail(STS_ERR_NOMEM, "bf16 mirror allocation of %llu bytes failed",
+                  (unsigned long long)(2 * n * sizeof(uint16_t)));
+    }
+    STS_HIP(hipMemsetAsync(c->k16, 0, n * sizeof(uint16_t), stream));
+    STS_HIP(hipMemsetAsync(c->v16, 0, n * sizeof(uint16_t), stream));
+  }
   // Zero-filled like Tensor::zeros (model.rs:272-279).
   STS_HIP(hipMemsetAsync(c->k, 0, n * sizeof(float), stream));
   STS_HIP(hipMemsetAsync(c->v, 0, n * sizeof(float), stream));
   c->batch = batch;
   return STS_OK;
+}
+
+void kv_free(sts_kv_cache* c) {
+  for (void* ptr : {(void*)c->k, (void*)c->v, (void*)c->k16, (void*)c->v16})
+    if (ptr) (void)hipFree(ptr);
+  c->k = c->v = nullptr;
+  c->k16 = c->v16 = nullptr;
 }
 
 }  // namespace
@@ -258,6 +281,34 @@ int sts_prefill_attention(const float* q, const float* k_cache, const float* v_c
   return sts::launch_prefill(p, head_dim, precision, as_stream(stream));
 }
 
+int sts_prefill_attention_bf16kv(const float* q, const uint16_t* k16, const uint16_t* v16,
+                                 float* out, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                                 uint32_t max_len, uint32_t win_start, uint32_t win_len,
+                                 float scale, void* stream) {
+  sts::clear_error();
+  STS_CHECK(q && k16 && v16 && out, "null pointer argument");
+  STS_CHECK(heads >= 1 && max_len >= 1, "empty shape");
+  STS_CHECK(seq >= 1 && seq <= win_len, "need 1 <= seq (%u) <= win_len (%u)", seq, win_len);
+  STS_CHECK(win_len <= max_len, "win_len %u > max_len %u", win_len, max_len);
+  STS_CHECK(win_start < max_len, "win_start %u >= max_len %u", win_start, max_len);
+  if (int rc = sts::check_prefill(seq, heads, head_dim, max_len, STS_PREC_BF16_MFMA)) return rc;
+  STS_CHECK(aligned16(q) && aligned16(k16) && aligned16(v16) && aligned16(out),
+            "pointers must be 16-byte aligned");
+  STS_CHECK(std::isfinite(scale), "scale must be finite");
+  sts::PrefillParams p;
+  p.q = q;
+  p.k16 = k16;
+  p.v16 = v16;
+  p.out = out;
+  p.S = seq;
+  p.H = heads;
+  p.M = max_len;
+  p.start = win_start;
+  p.len = win_len;
+  p.scale_log2 = sts::softmax_scale_log2(scale);
+  return sts::launch_prefill(p, head_dim, STS_PREC_BF16_MFMA, as_stream(stream));
+}
+
 /* ---------------------------------------------------------------------- */
 /* RoPE                                                                     */
 /* ---------------------------------------------------------------------- */
@@ -331,7 +382,13 @@ int sts_rope_apply(const sts_rope* rope, float* x, uint32_t batch, uint32_t seq,
 /* ---------------------------------------------------------------------- */
 
 int sts_kv_create(uint64_t max_len, uint64_t heads, uint64_t head_dim, sts_kv_cache** out) {
+  return sts_kv_create_ex(max_len, heads, head_dim, 0, out);
+}
+
+int sts_kv_create_ex(uint64_t max_len, uint64_t heads, uint64_t head_dim, uint32_t flags,
+                     sts_kv_cache** out) {
   sts::clear_error();
+  STS_CHECK((flags & ~(uint32_t)STS_KV_BF16_MIRROR) == 0, "unknown flags 0x%x", flags);
   STS_CHECK(out, "null out pointer");
   *out = nullptr;
   STS_CHECK(max_len >= 1 && max_len <= 0x7fffffffull, "max_len must be in 1..2^31-1");
@@ -342,6 +399,7 @@ int sts_kv_create(uint64_t max_len, uint64_t heads, uint64_t head_dim, sts_kv_ca
   c->max_len = max_len;
   c->heads = heads;
   c->head_dim = head_dim;
+  c->flags = flags;
   *out = c;
   return STS_OK;
 }
@@ -349,10 +407,26 @@ int sts_kv_create(uint64_t max_len, uint64_t heads, uint64_t head_dim, sts_kv_ca
 int sts_kv_destroy(sts_kv_cache* cache) {
   sts::clear_error();
   if (!cache) return STS_OK;
-  if (cache->k) (void)hipFree(cache->k);
-  if (cache->v) (void)hipFree(cache->v);
+  kv_free(cache);
   delete cache;
   return STS_OK;
+}
+
+int sts_kv_mirror(const sts_kv_cache* cache, uint16_t** k16, uint16_t** v16) {
+  sts::clear_error();
+  STS_CHECK(cache && k16 && v16, "null pointer argument");
+  *k16 = cache->k16;
+  *v16 = cache->v16;
+  return STS_OK;
+}
+
+int sts_kv_sync_mirror(sts_kv_cache* cache, void* stream) {
+  sts::clear_error();
+  STS_CHECK(cache, "null cache handle");
+  if (!cache->k16) return STS_OK;
+  const uint64_t n = cache->batch * cache->heads * cache->max_len * cache->head_dim;
+  if (int rc = sts::launch_to_bf16(cache->k, cache->k16, n, as_stream(stream))) return rc;
+  return sts::launch_to_bf16(cache->v, cache->v16, n, as_stream(stream));
 }
 
 int sts_kv_ensure_allocated(sts_kv_cache* cache, uint64_t batch, float** k, float** v,
@@ -378,6 +452,7 @@ int sts_kv_get_state(const sts_kv_cache* cache, sts_kv_state* out) {
   out->head_dim = cache->head_dim;
   out->batch = cache->batch;
   out->allocated = cache->k != nullptr;
+  out->flags = (int32_t)cache->flags;
   return STS_OK;
 }
 
@@ -408,12 +483,14 @@ int sts_kv_update(sts_kv_cache* cache, const float* k_new, const float* v_new, u
   // and offset agree modulo max_len under advance and rollback.
   const uint32_t pos = (uint32_t)(cache->offset % cache->max_len);
   if (aligned16(k_new) && aligned16(v_new)) {
-    // K and V in one launch.
+    // K and V (and their bf16 mirror) in one launch.
     if (int rc = sts::launch_kv_append(k_new, v_new, cache->k, cache->v, pos, (uint32_t)batch,
                                        (uint32_t)seq, (uint32_t)cache->heads,
                                        (uint32_t)cache->head_dim, (uint32_t)cache->max_len,
-                                       nullptr, nullptr, 0, s))
+                                       nullptr, nullptr, 0, cache->k16, cache->v16, s))
       return rc;
+  } else if (cache->k16) {
+    return fail(STS_ERR_INVALID, "a cache with a bf16 mirror needs 16-byte aligned k_new, v_new");
   } else {
     if (int rc = sts::launch_cache_write(k_new, cache->k, pos, (uint32_t)batch, (uint32_t)seq,
                                          (uint32_t)cache->heads, (uint32_t)cache->head_dim,
@@ -431,9 +508,7 @@ int sts_kv_update(sts_kv_cache* cache, const float* k_new, const float* v_new, u
 int sts_kv_reset(sts_kv_cache* cache) {
   sts::clear_error();
   STS_CHECK(cache, "null cache handle");
-  if (cache->k) STS_HIP(hipFree(cache->k));
-  if (cache->v) STS_HIP(hipFree(cache->v));
-  cache->k = cache->v = nullptr;
+  kv_free(cache);
   cache->batch = 0;
   cache->offset = cache->len = cache->write_pos = 0;
   return STS_OK;
@@ -446,6 +521,10 @@ int sts_kv_reset_keep_buffers(sts_kv_cache* cache, void* stream) {
     const uint64_t n = cache->batch * cache->heads * cache->max_len * cache->head_dim;
     STS_HIP(hipMemsetAsync(cache->k, 0, n * sizeof(float), as_stream(stream)));
     STS_HIP(hipMemsetAsync(cache->v, 0, n * sizeof(float), as_stream(stream)));
+    if (cache->k16) {
+      STS_HIP(hipMemsetAsync(cache->k16, 0, n * sizeof(uint16_t), as_stream(stream)));
+      STS_HIP(hipMemsetAsync(cache->v16, 0, n * sizeof(uint16_t), as_stream(stream)));
+    }
   }
   cache->offset = cache->len = cache->write_pos = 0;
   return STS_OK;
@@ -522,6 +601,8 @@ int sts_kv_decode_step(sts_kv_cache* cache, const sts_rope* rope, const float* q
   p.v_new = v_new;
   p.k_wr = cache->k;
   p.v_wr = cache->v;
+  p.k16_wr = cache->k16;
+  p.v16_wr = cache->v16;
   p.len = (uint32_t)next.len;
   p.start = (uint32_t)kv_start(&next);
   if (rope) {
@@ -572,7 +653,8 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
   if (int rc = sts::launch_kv_append(k_new, v_new, cache->k, cache->v, pos, 1, (uint32_t)seq,
                                      (uint32_t)cache->heads, (uint32_t)cache->head_dim,
                                      (uint32_t)cache->max_len, rope ? rope->cos_t : nullptr,
-                                     rope ? rope->sin_t : nullptr, (uint32_t)cache->offset, s))
+                                     rope ? rope->sin_t : nullptr, (uint32_t)cache->offset,
+                                     cache->k16, cache->v16, s))
     return rc;
   const uint64_t q_pos0 = cache->offset;
   *cache = next;
@@ -592,6 +674,12 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
     p.rope_cos = rope->cos_t;
     p.rope_sin = rope->sin_t;
     p.rope_pos0 = (uint32_t)q_pos0;
+  }
+  if (precision == STS_PREC_BF16_MFMA && cache->k16) {
+    // The mirror holds exactly the bf16 values the kernel would round the f32
+    // rows to: same result, half the K/V bytes.
+    p.k16 = cache->k16;
+    p.v16 = cache->v16;
   }
   return sts::launch_prefill(p, (uint32_t)cache->head_dim, precision, s);
 }

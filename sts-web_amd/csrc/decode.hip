@@ -262,6 +262,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       slot = slot >= p.M ? slot - p.M : slot;
       st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
       st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
+      if (p.k16_wr) {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const bf16x4 kb = {(__bf16)kn.x, (__bf16)kn.y, (__bf16)kn.z, (__bf16)kn.w};
+        const bf16x4 vb = {(__bf16)vn.x, (__bf16)vn.y, (__bf16)vn.z, (__bf16)vn.w};
+        *reinterpret_cast<bf16x4*>(p.k16_wr + kvoff + (size_t)slot * D + c * 4) = kb;
+        *reinterpret_cast<bf16x4*>(p.v16_wr + kvoff + (size_t)slot * D + c * 4) = vb;
+      }
     }
   };
   // One batch of 16 rows in flight per wave (16 KB, 64 KB per CU): loads,

@@ -20,6 +20,8 @@ struct DecodeParams {
   const float* v_new = nullptr;
   float* k_wr = nullptr;
   float* v_wr = nullptr;
+  uint16_t* k16_wr = nullptr;  // bf16 copies of k_wr/v_wr (same layout) that the
+  uint16_t* v16_wr = nullptr;  // appended row also goes to, rounded, or null
   const float* rope_cos = nullptr;  // [max_pos][D/2]; with rope, q and k_new are
   const float* rope_sin = nullptr;  // rotated in registers at position rope_pos
   const int32_t* lens = nullptr;    // per-stream device arrays, or null for the

@@ -506,6 +506,8 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
 // work instead of alternating with it at workgroup barriers.
 constexpr int kWsStages = 4;
 constexpr int kWsKB = 64;
+// Lazy rescaling threshold of the bf16 kernels' online softmax (log2 units).
+constexpr float kLazyLog2 = 8.f;
 
 // SPLIT stages hold two bf16 planes of every value, x_hi = bf16(x) and
 // x_lo = bf16(x - x_hi) (16 significant bits between them).
@@ -564,8 +566,16 @@ __device__ __forceinline__ void ws_signal(uint32_t* ctr, int lane) {
 // on this chip's 16:1 bf16:f32 matrix rate is ~5x the f32 MFMA rate.  Two
 // stages (the planes double a stage) and no LDS query tile: the consumers
 // split their own queries.
-template <int D, bool SPLIT>
+// KV16: the K/V rows come from bf16 copies of the caches (p.k16, p.v16,
+// [H][M][D] bf16, rounded to nearest even as the f32 path rounds them in its
+// producers), so the producers move half the bytes and convert nothing; the
+// stages, and therefore the result, are those of the f32-input kernel.
+template <int D, bool SPLIT, bool KV16 = false>
 __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) {
+  static_assert(!(SPLIT && KV16), "the split variant needs the f32 rows");
+  // Consumers one block ahead where the registers allow it (the bf16-input
+  // producers hold half the bytes of the f32-input ones).
+  constexpr bool PIPE = KV16;
   using Stage = WsStage<D, SPLIT>;
   constexpr int KB = kWsKB;
   constexpr int NS = SPLIT ? 2 : kWsStages;
@@ -619,7 +629,144 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
 
-  if (wave >= 4) {
+  if (wave >= 4 && KV16) {
+    // ---- producers, bf16 rows ----
+    const int pt = tid - 256;
+    constexpr int C8 = D / 8;               // 16-byte chunks (8 dims) of a bf16 row
+    constexpr int KP16 = KB * C8 / NP;      // K chunks per producer thread and block
+    constexpr int VQ16 = (KB / 4) * C8;     // V pieces (4 keys x 8 dims) per block
+    constexpr int VP16 = VQ16 >= NP ? VQ16 / NP : 1;
+    static_assert(KP16 >= 1 && (VQ16 % NP == 0 || NP % VQ16 == 0), "bf16 tile shape");
+    constexpr uint32_t ROWB = D * 2;
+    const int c8 = pt % C8;
+    const __amdgpu_buffer_rsrc_t k16rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<uint16_t*>(const_cast<void*>(p.k16)) + (size_t)h * p.M * D, 0,
+        (int)(p.M * ROWB), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t v16rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<uint16_t*>(const_cast<void*>(p.v16)) + (size_t)h * p.M * D, 0,
+        (int)(p.M * ROWB), kBufferWord3);
+    const bool v_thread = VQ16 >= NP || pt < VQ16;
+    auto k_row = [&](int i) { return (uint32_t)(pt / C8 + i * (NP / C8)); };
+    auto v_row = [&](int i, int r4) { return (uint32_t)((pt / C8 + i * (NP / C8)) * 4 + r4); };
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    struct Buf {
+      u32x4 k[KP16];
+      u32x4 v[VP16][4];
+    };
+    constexpr int NL = KP16 + 4 * VP16;
+    auto fetch = [&](Buf& bf, uint32_t b) {
+      const uint32_t kb = b * KB;
+      const uint32_t lim = b < nblk ? kend : 0u;
+      uint32_t slot0 = p.start + kb;
+      slot0 = slot0 >= p.M ? slot0 - p.M : slot0;
+      uint32_t vo[NL];
+      uint32_t so = 0;
+      if (kb + KB <= lim && slot0 + KB <= p.M) {
+        so = slot0 * ROWB;
+#pragma unroll
+        for (int i = 0; i < KP16; ++i) vo[i] = k_row(i) * ROWB + c8 * 16;
+#pragma unroll
+        for (int i = 0; i < VP16; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) vo[KP16 + 4 * i + r4] = v_row(i, r4) * ROWB + c8 * 16;
+      } else {
+        auto off = [&](uint32_t r) {
+          const uint32_t row = kb + r;
+          uint32_t slot = slot0 + r;
+          slot = min(slot, slot - p.M);  // wrap (slot < 2M)
+          return row < lim ? slot * ROWB + c8 * 16 : 0xFFFFFFF0u;
+        };
+#pragma unroll
+        for (int i = 0; i < KP16; ++i) vo[i] = off(k_row(i));
+#pragma unroll
+        for (int i = 0; i < VP16; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) vo[KP16 + 4 * i + r4] = off(v_row(i, r4));
+      }
+#pragma unroll
+      for (int i = 0; i < KP16; ++i)
+        bf.k[i] = __builtin_amdgcn_raw_buffer_load_b128(k16rs, vo[i], so, 0);
+      if (v_thread) {
+#pragma unroll
+        for (int i = 0; i < VP16; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            bf.v[i][r4] = __builtin_amdgcn_raw_buffer_load_b128(v16rs, vo[KP16 + 4 * i + r4], so, 0);
+      }
+    };
+    // K chunks go to their rows as they are; each V piece (4 keys x 8 dims) is
+    // transposed into 8 runs of 4 keys (dims c8*8 .. +7).
+    auto put = [&](const Buf& bf, Stage& sg) {
+#pragma unroll
+      for (int i = 0; i < KP16; ++i)
+        *reinterpret_cast<u32x4*>(&sg.ks[0][k_row(i) * KP + c8 * 8]) = bf.k[i];
+      if (!v_thread) return;
+#pragma unroll
+      for (int i = 0; i < VP16; ++i) {
+        const int key0 = (pt / C8 + i * (NP / C8)) * 4;
+        const u32x4* x = bf.v[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = c8 * 8 + e;
+          const int w = e >> 1, sh = (e & 1) * 16;
+          const uint32_t r0 = (x[0][w] >> sh) & 0xFFFFu, r1 = (x[1][w] >> sh) & 0xFFFFu;
+          const uint32_t r2 = (x[2][w] >> sh) & 0xFFFFu, r3 = (x[3][w] >> sh) & 0xFFFFu;
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2*>(&sg.vt[0][d * VP + ws_vt_pos(d, key0)]) =
+              u32x2{r0 | (r1 << 16), r2 | (r3 << 16)};
+        }
+      }
+    };
+    auto produce = [&](const Buf& bf, uint32_t i) {
+      const uint32_t s = i % NS, use = i / NS;
+      ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane, p.err);
+      put(bf, st[s]);
+      ws_signal(&filled[s], lane);
+    };
+    // Queries: as the f32 producers stage them.
+    constexpr int QPER = QT * C4 / NP;
+    const int d4 = pt % C4;
+    auto q_row = [&](int i) { return (uint32_t)(pt / C4 + i * (NP / C4)); };
+    float4 qv[QPER];
+#pragma unroll
+    for (int i = 0; i < QPER; ++i) {
+      const uint32_t qq = qt * QT + q_row(i);
+      qv[i] = ld4(p.q + ((size_t)(qq < p.S ? qq : 0) * p.H + h) * D + d4 * 4);
+    }
+    float2 qcs[QPER], qsn[QPER];
+    if (p.rope_cos) {
+#pragma unroll
+      for (int i = 0; i < QPER; ++i) {
+        const uint32_t qq = qt * QT + q_row(i);
+        rope_coeffs<D>(p.rope_cos, p.rope_sin, p.rope_pos0 + (qq < p.S ? qq : 0), d4 * 4, qcs[i],
+                       qsn[i]);
+      }
+    }
+    Buf b0, b1, b2;
+    fetch(b0, 0);
+    fetch(b1, 1);
+#pragma unroll
+    for (int i = 0; i < QPER; ++i) {
+      const uint32_t qq = qt * QT + q_row(i);
+      if (p.rope_cos) qv[i] = rope4(qv[i], qcs[i], qsn[i]);
+      const float4 x = scale4(qv[i], qq < p.S ? p.scale_log2 : 0.f);
+      bf16x4 y;
+      y[0] = (__bf16)x.x; y[1] = (__bf16)x.y; y[2] = (__bf16)x.z; y[3] = (__bf16)x.w;
+      *reinterpret_cast<bf16x4*>(&qs[q_row(i) * QP + d4 * 4]) = y;
+    }
+    ws_signal(&q_ready, lane);
+    produce(b0, 0);
+    for (uint32_t i = 1; i < nblk; i += 3) {
+      fetch(b2, i + 1);
+      produce(b1, i);
+      if (i + 1 >= nblk) break;
+      fetch(b0, i + 2);
+      produce(b2, i + 1);
+      if (i + 2 >= nblk) break;
+      fetch(b1, i + 3);
+      produce(b0, i + 2);
+    }
+  } else if (wave >= 4) {
     // ---- producers ----
     const int pt = tid - 256;
     const int d4 = pt % C4;
@@ -803,11 +950,11 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       for (int a = 0; a < KA; ++a)
         qop[0][a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
     }
-    for (uint32_t i = 0; i < nblk; ++i) {
+    // Scores S^T of block i: waits for its stage, K operands from LDS, MFMAs.
+    auto s_block = [&](uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane, p.err);
       const Stage& sg = st[s];
-      const uint32_t k0 = i * KB + ks * 32;
       f32x16 sc;
 #pragma unroll
       for (int v = 0; v < 16; ++v) sc[v] = 0.f;
@@ -827,38 +974,45 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[a], qop[QPL - 1][a], sc, 0, 0, 0);
         }
       }
-
+      return sc;
+    };
+    // Mask, online softmax and O^T += V^T P^T of block i; releases its stage.
+    auto finish_block = [&](uint32_t i, f32x16 sc) {
+      const uint32_t s = i % NS;
+      const Stage& sg = st[s];
+      const uint32_t k0 = i * KB + ks * 32;
       const bool unmasked = k0 + 31 < kend && k0 + 31 <= w_first;
-      float mx = -INFINITY;
-      if (unmasked) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[v]);
-      } else {
+      if (!unmasked) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const uint32_t key = k0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-          const float x = (key <= w_q && key < kend) ? sc[v] : -INFINITY;
-          sc[v] = x;
-          mx = fmaxf(mx, x);
+          sc[v] = (key <= w_q && key < kend) ? sc[v] : -INFINITY;
         }
       }
-      mx = max_xor32(mx);
-      const float mn = fmaxf(m, mx);
-      const float alpha = fast_exp2(m - mn);
-      m = mn;
-      float ps = 0.f;
+      float mx = sc[0];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float e = fast_exp2(sc[v] - mn);
-        sc[v] = e;
-        ps += e;
-      }
-      ps = sum_xor32(ps);
-      lsum = lsum * alpha + ps;
-      if (__any(alpha != 1.f)) {
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[v]);
+      mx = max_xor32(mx);
+      // Lazy rescaling: the weights stay relative to the base m until some
+      // query's block maximum exceeds it by more than kLazyLog2 (weights then
+      // stay <= 2^kLazyLog2); only then does the base move and O get
+      // rescaled.  The same softmax; the rescale no longer runs every block.
+      if (__any(mx > m + kLazyLog2)) {
+        const float mn = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - mn);
+        m = mn;
+        lsum *= alpha;
 #pragma unroll
         for (int t = 0; t < OT; ++t) o[t] *= alpha;
       }
+      float ps = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float e = fast_exp2(sc[v] - m);
+        sc[v] = e;
+        ps += e;
+      }
+      lsum += sum_xor32(ps);
       bf16x8 pb[QPL][2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -891,6 +1045,20 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         }
       }
       ws_signal(&released[s], lane);
+    };
+    if constexpr (PIPE) {
+      // One block ahead: the next block's score MFMAs are issued before this
+      // block's softmax, so the matrix pipe works while the VALU does the
+      // softmax (the consumers hold two stages at a time).
+      f32x16 sc = s_block(0);
+      for (uint32_t i = 0; i < nblk; ++i) {
+        f32x16 sn = sc;
+        if (i + 1 < nblk) sn = s_block(i + 1);
+        finish_block(i, sc);
+        sc = sn;
+      }
+    } else {
+      for (uint32_t i = 0; i < nblk; ++i) finish_block(i, s_block(i));
     }
   }
 
@@ -930,13 +1098,14 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     }
 }
 
-template <int D, bool SPLIT>
+template <int D, bool SPLIT, bool KV16 = false>
 int launch_ws(const PrefillParams& p, hipStream_t stream) {
   const uint32_t nqt = (p.S + 63) / 64;
   if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
   if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
-  hipLaunchKernelGGL((prefill_ws_kernel<D, SPLIT>), dim3(p.H, nqt, 1), dim3(512), 0, stream, p);
+  hipLaunchKernelGGL((prefill_ws_kernel<D, SPLIT, KV16>), dim3(p.H, nqt, 1), dim3(512), 0, stream,
+                     p);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }
@@ -991,6 +1160,13 @@ int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hi
   p.wait_limit = wait_limit();
   if (int rc = device_error_word(&p.err)) return rc;
   const bool d128 = head_dim == 128;
+  if (!(p.k16 && p.v16) && !(p.k && p.v))
+    return fail(STS_ERR_INVALID, "prefill needs the K/V caches (f32 or their bf16 copies)");
+  if (p.k16) {
+    if (precision != STS_PREC_BF16_MFMA)
+      return fail(STS_ERR_INVALID, "bf16 K/V rows serve the bf16-MFMA precision only");
+    return d128 ? launch_ws<128, false, true>(p, stream) : launch_ws<64, false, true>(p, stream);
+  }
   switch (precision) {
     case STS_PREC_BF16_MFMA:
       return d128 ? launch_ws<128, false>(p, stream) : launch_ws<64, false>(p, stream);

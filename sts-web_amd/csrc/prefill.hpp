@@ -33,6 +33,10 @@ struct PrefillParams {
   // STS_DEVERR_WAIT_TIMEOUT in the device error word.
   uint32_t wait_limit = 1u << 24;
   uint32_t* err = nullptr;  // the device error word
+  // bf16 copies of the caches ([H][M][D], bf16 bits); when set, the bf16-MFMA
+  // kernel reads them instead of k / v.
+  const void* k16 = nullptr;
+  const void* v16 = nullptr;
 };
 
 // Checks everything launch_prefill would reject for these sizes, without

@@ -37,6 +37,7 @@ DEVERR_WAIT_TIMEOUT = 1
 PREC_F32 = 0
 PREC_BF16_MFMA = 1
 PREC_F32_SPLIT_BF16 = 2
+KV_BF16_MIRROR = 1
 
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32
@@ -54,7 +55,7 @@ class StsError(RuntimeError):
 class KvState(ctypes.Structure):
     _fields_ = [("offset", _u64), ("len", _u64), ("write_pos", _u64), ("max_len", _u64),
                 ("heads", _u64), ("head_dim", _u64), ("batch", _u64), ("allocated", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("flags", ctypes.c_int32)]
 
 
 # name -> (restype, argtypes); the exported set of include/sts_attn.h.
@@ -74,6 +75,11 @@ SIGNATURES = {
     "sts_rope_destroy": (_int, [_vp]),
     "sts_rope_apply": (_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "sts_kv_create": (_int, [_u64, _u64, _u64, ctypes.POINTER(_vp)]),
+    "sts_kv_create_ex": (_int, [_u64, _u64, _u64, _u32, ctypes.POINTER(_vp)]),
+    "sts_kv_mirror": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+    "sts_kv_sync_mirror": (_int, [_vp, _vp]),
+    "sts_prefill_attention_bf16kv": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+                                            _u32, _f32, _vp]),
     "sts_kv_destroy": (_int, [_vp]),
     "sts_kv_ensure_allocated": (_int, [_vp, _u64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                        ctypes.POINTER(_u64), _vp]),
@@ -231,6 +237,24 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
+def prefill_attention_bf16kv(q: torch.Tensor, k16: torch.Tensor, v16: torch.Tensor,
+                             win_start: int, win_len: int, scale: float,
+                             out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Causal chunk attention (bf16 MFMA) over bf16 copies of the caches: q [S,H,D]
+    f32, k16/v16 [H,M,D] (or [1,H,M,D]) torch.bfloat16 or int16 bit patterns."""
+    S, H, D = q.shape
+    M = k16.shape[-2]
+    for t in (k16, v16):
+        if t.dtype not in (torch.bfloat16, torch.int16) or not t.is_contiguous():
+            raise ValueError("k16/v16 must be contiguous bfloat16 (or int16 bits)")
+    if out is None:
+        out = torch.empty_like(q)
+    _check(load().sts_prefill_attention_bf16kv(_ptr(q), k16.data_ptr(), v16.data_ptr(), _ptr(out),
+                                               S, H, D, M, win_start, win_len, scale,
+                                               _stream(stream)))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # RoPE
 # ---------------------------------------------------------------------------
@@ -279,9 +303,10 @@ class RoPE:
 class KVCache:
     """Ring-buffer KV cache in HBM, KVCache (model.rs:195-363)."""
 
-    def __init__(self, max_len: int, n_kv_heads: int, head_dim: int):
+    def __init__(self, max_len: int, n_kv_heads: int, head_dim: int, bf16_mirror: bool = False):
         h = _vp()
-        _check(load().sts_kv_create(max_len, n_kv_heads, head_dim, ctypes.byref(h)))
+        _check(load().sts_kv_create_ex(max_len, n_kv_heads, head_dim,
+                                       KV_BF16_MIRROR if bf16_mirror else 0, ctypes.byref(h)))
         self._h = h
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim
@@ -327,6 +352,21 @@ class KVCache:
         kp, vp, _ = self.ensure_allocated(s.batch)
         shape = (s.batch, s.heads, s.max_len, s.head_dim)
         return copy_device(kp, shape), copy_device(vp, shape)
+
+    def mirror_buffers(self):
+        """Copies of the bf16 mirror [B, H, max_len, D] (torch.int16 bit patterns),
+        or (None, None) when there is none."""
+        s = self.state()
+        kp, vp = _vp(), _vp()
+        _check(load().sts_kv_mirror(self._h, ctypes.byref(kp), ctypes.byref(vp)))
+        if not kp.value:
+            return None, None
+        shape = (s.batch, s.heads, s.max_len, s.head_dim)
+        return (copy_device(kp.value, shape, torch.int16),
+                copy_device(vp.value, shape, torch.int16))
+
+    def sync_mirror(self, stream=None) -> None:
+        _check(load().sts_kv_sync_mirror(self._h, _stream(stream)))
 
     def advance(self, num_steps: int) -> None:
         _check(load().sts_kv_advance(self._h, num_steps))
@@ -432,11 +472,11 @@ def _hip():
     return _hiprt
 
 
-def copy_device(ptr: int, shape: Sequence[int]) -> torch.Tensor:
-    """A float32 torch copy of `shape` elements at device address `ptr`."""
-    t = torch.empty(tuple(shape), dtype=torch.float32, device="cuda")
+def copy_device(ptr: int, shape: Sequence[int], dtype=torch.float32) -> torch.Tensor:
+    """A torch copy of `shape` elements of `dtype` at device address `ptr`."""
+    t = torch.empty(tuple(shape), dtype=dtype, device="cuda")
     torch.cuda.synchronize()
-    rc = _hip().hipMemcpy(t.data_ptr(), ptr, t.numel() * 4, 3)  # hipMemcpyDeviceToDevice
+    rc = _hip().hipMemcpy(t.data_ptr(), ptr, t.numel() * t.element_size(), 3)  # device to device
     if rc != 0:
         raise StsError(STS_ERR_HIP, f"hipMemcpy failed with code {rc}")
     return t
