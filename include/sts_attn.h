@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define STS_ATTN_ABI_VERSION 2
+#define STS_ATTN_ABI_VERSION 3
 
 enum sts_status {
   STS_OK = 0,
@@ -247,6 +247,7 @@ typedef struct sts_kv_state {
   uint64_t batch;     /* 0 until the buffers are allocated                 */
   int32_t allocated;  /* 1 when the K/V buffers exist                      */
   int32_t flags;      /* the sts_kv_create_ex flags (STS_KV_BF16_MIRROR)   */
+  uint64_t q_heads;   /* query heads of q/out (sts_kv_set_query_heads)     */
 } sts_kv_state;
 
 /* sts_kv_create_ex flag: keep a bf16 copy of K and V (see sts_kv_create_ex). */
@@ -277,6 +278,18 @@ int sts_kv_mirror(const sts_kv_cache* cache, uint16_t** k16, uint16_t** v16);
 
 /* Rebuilds the bf16 mirror from the f32 caches (after direct writes). */
 int sts_kv_sync_mirror(sts_kv_cache* cache, void* stream);
+
+/*
+ * Grouped-query attention (the prefill branch's K/V expansion,
+ * model.rs:766-783, which the reference also takes for S = 1 when
+ * n_heads != n_kv_heads, model.rs:739): the cache holds `heads` K/V heads and
+ * q / out of sts_kv_attend, sts_kv_decode_step and sts_kv_prefill have
+ * q_heads heads, a multiple of heads; query head h attends K/V head
+ * h / (q_heads / heads), i.e. each K/V head repeated for q_heads / heads
+ * consecutive query heads.  k_new / v_new keep `heads` heads.  The default
+ * is q_heads = heads.
+ */
+int sts_kv_set_query_heads(sts_kv_cache* cache, uint64_t q_heads);
 int sts_kv_destroy(sts_kv_cache* cache);
 
 /*
@@ -319,9 +332,10 @@ int sts_kv_rollback(sts_kv_cache* cache, uint64_t n);
 
 /*
  * Decode attention over the cache's current window for each stream of the
- * batch (equal lengths): q, out [batch][heads][head_dim].  This is
- * fused_attention(q, k_all, v_all) on the views advance() returns
- * (model.rs:829-831), generalised to a wrapped window.
+ * batch (equal lengths): q, out [batch][q_heads][head_dim] (q_heads = heads
+ * unless set by sts_kv_set_query_heads).  This is fused_attention(q, k_all,
+ * v_all) on the views advance() returns (model.rs:829-831), generalised to a
+ * wrapped window.
  */
 int sts_kv_attend(sts_kv_cache* cache, const float* q, float* out, float scale, void* stream);
 
@@ -330,7 +344,8 @@ int sts_kv_attend(sts_kv_cache* cache, const float* q, float* out, float scale, 
  * RoPE of q and k_new at position `offset`, append of k_new/v_new at slot
  * write_pos, advance(1), and attention over the new window -- the decode
  * branch of Q4Attention::forward_with_cache (model.rs:739-758, 818-835) in one
- * launch.  q, k_new, v_new, out are [batch][heads][head_dim].  `rope` may be
+ * launch.  q, out are [batch][q_heads][head_dim], k_new, v_new
+ * [batch][heads][head_dim].  `rope` may be
  * NULL (depformer, depth.rs:100); when given, q and k_new are read unrotated
  * and the rotated q is not written back.  Allocates the cache on first use.
  */
@@ -347,8 +362,9 @@ int sts_kv_decode_step(sts_kv_cache* cache, const sts_rope* rope, const float* q
  * ([seq][heads][head_dim]) at slots (offset+s) % max_len in one launch, and q
  * in registers inside the attention kernel (the rotated q is not written
  * back).  With rope NULL, q and k_new are taken as already rotated.  Then
- * causal attention of the `seq` queries q [seq][heads][head_dim] over the
- * grown window into out.  Every argument is checked before anything is
+ * causal attention of the `seq` queries q [seq][q_heads][head_dim] over the
+ * grown window into out (with q_heads > heads, grouped-query attention as
+ * sts_kv_set_query_heads describes).  Every argument is checked before anything is
  * written: a rejected call leaves the cache and its counters unchanged.
  * q, k_new, v_new, out 16-byte aligned; offset+seq must not exceed the RoPE
  * table.

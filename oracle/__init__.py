@@ -58,6 +58,7 @@ def _load():
         "orc_rope_tables": (None, [_u32, _u32, ctypes.c_float, _f32p, _f32p]),
         "orc_rope_apply": (None, [_f32p, _u32, _u32, _u32, _u32, _u32, _f32p, _f32p]),
         "orc_cache_write": (None, [_f32p, _f32p, _u32, _u32, _u32, _u32, _u32, _u32]),
+        "orc_gqa_expand": (None, [_f32p, _f32p, _u32, _u32, _u32, _u64]),
         "orc_kv_init": (None, [ctypes.POINTER(KvState), _u64]),
         "orc_kv_advance": (None, [ctypes.POINTER(KvState), _u64]),
         "orc_kv_update": (None, [ctypes.POINTER(KvState)]),
@@ -168,6 +169,18 @@ def cache_write(inp: np.ndarray, cache: np.ndarray, pos_offset: int, max_len: in
     assert cache.shape == (B, H, max_len, D)
     lib().orc_cache_write(_p32(np.ascontiguousarray(inp)), _p32(cache), pos_offset, B, S, H, D,
                           max_len)
+
+
+def gqa_expand(kv: np.ndarray, rep: int) -> np.ndarray:
+    """K/V heads repeated for grouped-query attention (model.rs:766-783):
+    kv [..., nkv, S, D] -> [..., nkv * rep, S, D], head j * rep + r = head j.
+    The leading axes (if any) are batch."""
+    kv = np.ascontiguousarray(kv, np.float32)
+    *lead, nkv, S, D = kv.shape
+    B = int(np.prod(lead)) if lead else 1
+    out = np.empty((*lead, nkv * rep, S, D), np.float32)
+    lib().orc_gqa_expand(_p32(kv), _p32(out), B, nkv, rep, S * D)
+    return out
 
 
 class KvCounters:

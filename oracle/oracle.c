@@ -129,6 +129,21 @@ void orc_cache_write(const float* input, float* cache, uint32_t pos_offset,
   }
 }
 
+/* The grouped-query expansion of the prefill branch (model.rs:766-783):
+ * k [B][nkv][S][hd] -> unsqueeze_dim(2) -> repeat_dim(2, rep) -> reshape
+ * [B][nkv * rep][S][hd], so expanded head h = j * rep + r holds K/V head j.
+ * `rows` is S * hd floats per head. */
+void orc_gqa_expand(const float* kv, float* out, uint32_t B, uint32_t nkv, uint32_t rep,
+                    uint64_t rows) {
+  for (uint32_t b = 0; b < B; ++b)
+    for (uint32_t j = 0; j < nkv; ++j)
+      for (uint32_t r = 0; r < rep; ++r) {                         /* :772-775 */
+        const float* src = kv + ((uint64_t)b * nkv + j) * rows;
+        float* dst = out + (((uint64_t)b * nkv + j) * rep + r) * rows;  /* :776 reshape */
+        for (uint64_t i = 0; i < rows; ++i) dst[i] = src[i];
+      }
+}
+
 void orc_kv_init(orc_kv* c, uint64_t max_len) {  /* model.rs:207-219 */
   c->offset = 0;
   c->len = 0;

@@ -50,6 +50,11 @@ void orc_rope_apply(float* x, uint32_t B, uint32_t S, uint32_t H, uint32_t D,
 void orc_cache_write(const float* input, float* cache, uint32_t pos_offset,
                      uint32_t B, uint32_t S, uint32_t H, uint32_t D, uint32_t max_len);
 
+/* ---- GQA expansion of K/V heads (model.rs:766-783) ----------------------- */
+
+void orc_gqa_expand(const float* kv, float* out, uint32_t B, uint32_t nkv, uint32_t rep,
+                    uint64_t rows);
+
 /* ---- KV cache counters (model.rs:195-363) -------------------------------- */
 
 typedef struct orc_kv {

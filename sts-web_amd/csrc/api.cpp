@@ -28,6 +28,7 @@ struct sts_rope {
 
 struct sts_kv_cache {
   uint64_t max_len = 0, heads = 0, head_dim = 0;
+  uint64_t q_heads = 0;  // query heads of q/out (a multiple of heads: GQA)
   uint64_t offset = 0, len = 0, write_pos = 0;
   uint64_t batch = 0;
   uint32_t flags = 0;
@@ -398,9 +399,20 @@ int sts_kv_create_ex(uint64_t max_len, uint64_t heads, uint64_t head_dim, uint32
   if (!c) return fail(STS_ERR_NOMEM, "host allocation failed");
   c->max_len = max_len;
   c->heads = heads;
+  c->q_heads = heads;
   c->head_dim = head_dim;
   c->flags = flags;
   *out = c;
+  return STS_OK;
+}
+
+int sts_kv_set_query_heads(sts_kv_cache* cache, uint64_t q_heads) {
+  sts::clear_error();
+  STS_CHECK(cache, "null cache handle");
+  STS_CHECK(q_heads >= cache->heads && q_heads <= 65535 && q_heads % cache->heads == 0,
+            "query heads %llu must be a multiple of the %llu K/V heads, at most 65535",
+            (unsigned long long)q_heads, (unsigned long long)cache->heads);
+  cache->q_heads = q_heads;
   return STS_OK;
 }
 
@@ -453,6 +465,7 @@ int sts_kv_get_state(const sts_kv_cache* cache, sts_kv_state* out) {
   out->batch = cache->batch;
   out->allocated = cache->k != nullptr;
   out->flags = (int32_t)cache->flags;
+  out->q_heads = cache->q_heads;
   return STS_OK;
 }
 
@@ -544,13 +557,18 @@ int sts_kv_rollback(sts_kv_cache* cache, uint64_t n) {
   return STS_OK;
 }
 
+// q/out hold the handle's query heads; K/V head j serves query heads
+// j * group .. j * group + group - 1 (model.rs:766-783's repeat of each K/V
+// head), k_new/v_new the K/V heads.
 static void fill_cache_decode(const sts_kv_cache* c, sts::DecodeParams& p) {
   p.k = c->k;
   p.v = c->v;
   p.M = (uint32_t)c->max_len;
-  p.H = (uint32_t)c->heads;
-  p.q_bstride = c->heads * c->head_dim;
-  p.out_bstride = c->heads * c->head_dim;
+  p.H = (uint32_t)c->q_heads;
+  p.group = (uint32_t)(c->q_heads / c->heads);
+  p.q_bstride = c->q_heads * c->head_dim;
+  p.out_bstride = c->q_heads * c->head_dim;
+  p.kn_bstride = c->heads * c->head_dim;
   p.kv_hstride = c->max_len * c->head_dim;
   p.kv_bstride = c->heads * c->max_len * c->head_dim;
 }
@@ -629,7 +647,7 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
   if (cache->k && cache->batch != 1)
     return fail(STS_ERR_STATE, "prefill needs a batch-1 cache (allocated with batch %llu)",
                 (unsigned long long)cache->batch);
-  if (int rc = sts::check_prefill((uint32_t)seq, (uint32_t)cache->heads,
+  if (int rc = sts::check_prefill((uint32_t)seq, (uint32_t)cache->q_heads,
                                   (uint32_t)cache->head_dim, (uint32_t)cache->max_len, precision))
     return rc;
   STS_CHECK(aligned16(q) && aligned16(k_new) && aligned16(v_new) && aligned16(out),
@@ -664,7 +682,8 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
   p.v = cache->v;
   p.out = out;
   p.S = (uint32_t)seq;
-  p.H = (uint32_t)cache->heads;
+  p.H = (uint32_t)cache->q_heads;
+  p.group = (uint32_t)(cache->q_heads / cache->heads);
   p.M = (uint32_t)cache->max_len;
   p.start = (uint32_t)kv_start(cache);
   p.len = (uint32_t)cache->len;

@@ -158,7 +158,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   q4.z *= p.scale_log2;
   q4.w *= p.scale_log2;
 
-  const size_t kvoff = b * p.kv_bstride + h * p.kv_hstride;
+  // The K/V head of this query head (no division on the common group-1 path).
+  const uint32_t kvh = p.group == 1 ? h : h / p.group;
+  const size_t kvoff = b * p.kv_bstride + kvh * p.kv_hstride;
   // K/V rows come in through buffer loads on per-(stream, head) resources:
   // a row outside the window gets an offset past the resource and loads
   // zeros, so every load is issued unconditionally and the compiler's wait
@@ -177,8 +179,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // the wave whose unit holds it, which also use it from registers.
   float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
   if (append) {
-    kn = ld4(p.k_new + qoff);
-    vn = ld4(p.v_new + qoff);
+    const size_t knoff = b * (p.kn_bstride ? p.kn_bstride : p.q_bstride) + (size_t)kvh * D + c * 4;
+    kn = ld4(p.k_new + knoff);
+    vn = ld4(p.v_new + knoff);
   }
 
   float m = -FLT_MAX;
@@ -258,16 +261,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       // Only these lanes wait for k_new and the table: the others go on to
       // their first loads.
       if (rope) kn = rope4(kn, rc, rs);
-      uint32_t slot = start + new_row;
-      slot = slot >= p.M ? slot - p.M : slot;
-      st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
-      st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
-      if (p.k16_wr) {
-        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-        const bf16x4 kb = {(__bf16)kn.x, (__bf16)kn.y, (__bf16)kn.z, (__bf16)kn.w};
-        const bf16x4 vb = {(__bf16)vn.x, (__bf16)vn.y, (__bf16)vn.z, (__bf16)vn.w};
-        *reinterpret_cast<bf16x4*>(p.k16_wr + kvoff + (size_t)slot * D + c * 4) = kb;
-        *reinterpret_cast<bf16x4*>(p.v16_wr + kvoff + (size_t)slot * D + c * 4) = vb;
+      // Every query head of a K/V group uses the row from registers; the
+      // group's first head stores it.
+      if (h == kvh * p.group) {
+        uint32_t slot = start + new_row;
+        slot = slot >= p.M ? slot - p.M : slot;
+        st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
+        st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
+        if (p.k16_wr) {
+          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+          const bf16x4 kb = {(__bf16)kn.x, (__bf16)kn.y, (__bf16)kn.z, (__bf16)kn.w};
+          const bf16x4 vb = {(__bf16)vn.x, (__bf16)vn.y, (__bf16)vn.z, (__bf16)vn.w};
+          *reinterpret_cast<bf16x4*>(p.k16_wr + kvoff + (size_t)slot * D + c * 4) = kb;
+          *reinterpret_cast<bf16x4*>(p.v16_wr + kvoff + (size_t)slot * D + c * 4) = vb;
+        }
       }
     }
   };
@@ -493,6 +500,8 @@ int check_decode(const DecodeParams& p, uint32_t batch, uint32_t head_dim) {
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
   if (batch > 65535u || p.H > 65535u)
     return fail(STS_ERR_INVALID, "batch (%u) and heads (%u) must be <= 65535", batch, p.H);
+  if (p.group == 0 || p.H % p.group != 0)
+    return fail(STS_ERR_INVALID, "query heads %u not a multiple of the K/V group %u", p.H, p.group);
   return STS_OK;
 }
 

@@ -7,16 +7,19 @@
 
 namespace sts {
 
-// One launch of the decode kernel.  Row i (0 <= i < len) of stream b, head h
-// lives in slot (start + i) % M of  k + b*kv_bstride + h*kv_hstride  (rows of
-// head_dim floats).  With k_new set, row len-1 is taken from k_new/v_new and
-// written to its slot of k_wr/v_wr (a fused append).
+// One launch of the decode kernel.  Row i (0 <= i < len) of stream b, query
+// head h lives in slot (start + i) % M of
+//   k + b*kv_bstride + (h / group)*kv_hstride
+// (rows of head_dim floats; group > 1 is grouped-query attention, each K/V
+// head serving `group` consecutive query heads).  With k_new set, row len-1
+// is taken from k_new/v_new and written to its slot of k_wr/v_wr (a fused
+// append; with group > 1 by the first query head of each group only).
 struct DecodeParams {
   const float* q = nullptr;      // stream b, head h at q + b*q_bstride + h*D
   const float* k = nullptr;
   const float* v = nullptr;
   float* out = nullptr;          // stream b, head h at out + b*out_bstride + h*D
-  const float* k_new = nullptr;  // same addressing as q, or null
+  const float* k_new = nullptr;  // stream b, K/V head j at k_new + b*kn_bstride + j*D, or null
   const float* v_new = nullptr;
   float* k_wr = nullptr;
   float* v_wr = nullptr;
@@ -31,6 +34,8 @@ struct DecodeParams {
   uint32_t H = 0, M = 0;
   uint64_t q_bstride = 0, out_bstride = 0;
   uint64_t kv_bstride = 0, kv_hstride = 0;
+  uint64_t kn_bstride = 0;  // k_new/v_new stream stride; 0: q_bstride
+  uint32_t group = 1;       // query heads per K/V head
   float scale_log2 = 0.f;  // softmax scale * log2(e)
   uint32_t chunk = 0;      // rows per split
   uint32_t nsplit_max = 1; // grid x

@@ -116,6 +116,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   const int g = lane >> 4;
   const int l16 = lane & 15;
   const uint32_t h = blockIdx.x;
+  const uint32_t kvh = p.group == 1 ? h : h / p.group;  // its K/V head
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   const uint32_t qt = nqt - 1 - blockIdx.y;
   const uint32_t split = blockIdx.z;
@@ -166,9 +167,11 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   // zeros (finite, and masked out of the softmax).
   constexpr uint32_t ROWB = D * sizeof(float);
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(p.k) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+      const_cast<float*>(p.k) + (size_t)kvh * p.M * D, 0, (int)(p.M * ROWB),
+      kBufferWord3);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(p.v) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+      const_cast<float*>(p.v) + (size_t)kvh * p.M * D, 0, (int)(p.M * ROWB),
+      kBufferWord3);
   const bool v_thread = VSQ >= NT || tid < VSQ;
   auto k_row = [&](int i) { return (uint32_t)(tid / C4 + i * (NT / C4)); };
   auto v_row = [&](int i, int r4) { return (uint32_t)((tid / C4 + i * (NT / C4)) * 4 + r4); };
@@ -601,6 +604,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t h = blockIdx.x;
+  const uint32_t kvh = p.group == 1 ? h : h / p.group;  // its K/V head
   const uint32_t nqt = (p.S + QT - 1) / QT;
   const uint32_t qt = nqt - 1 - blockIdx.y;  // heaviest tiles first
   const uint32_t base_w = p.len - p.S;
@@ -640,11 +644,11 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     constexpr uint32_t ROWB = D * 2;
     const int c8 = pt % C8;
     const __amdgpu_buffer_rsrc_t k16rs = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<uint16_t*>(const_cast<void*>(p.k16)) + (size_t)h * p.M * D, 0,
-        (int)(p.M * ROWB), kBufferWord3);
+        reinterpret_cast<uint16_t*>(const_cast<void*>(p.k16)) + (size_t)kvh * p.M * D,
+        0, (int)(p.M * ROWB), kBufferWord3);
     const __amdgpu_buffer_rsrc_t v16rs = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<uint16_t*>(const_cast<void*>(p.v16)) + (size_t)h * p.M * D, 0,
-        (int)(p.M * ROWB), kBufferWord3);
+        reinterpret_cast<uint16_t*>(const_cast<void*>(p.v16)) + (size_t)kvh * p.M * D,
+        0, (int)(p.M * ROWB), kBufferWord3);
     const bool v_thread = VQ16 >= NP || pt < VQ16;
     auto k_row = [&](int i) { return (uint32_t)(pt / C8 + i * (NP / C8)); };
     auto v_row = [&](int i, int r4) { return (uint32_t)((pt / C8 + i * (NP / C8)) * 4 + r4); };
@@ -772,9 +776,11 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     const int d4 = pt % C4;
     constexpr uint32_t ROWB = D * sizeof(float);
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(p.k) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+        const_cast<float*>(p.k) + (size_t)kvh * p.M * D, 0, (int)(p.M * ROWB),
+        kBufferWord3);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(p.v) + (size_t)h * p.M * D, 0, (int)(p.M * ROWB), kBufferWord3);
+        const_cast<float*>(p.v) + (size_t)kvh * p.M * D, 0, (int)(p.M * ROWB),
+        kBufferWord3);
     const bool v_thread = VSQ >= NP || pt < VSQ;
     auto k_row = [&](int i) { return (uint32_t)(pt / C4 + i * (NP / C4)); };
     auto v_row = [&](int i, int r4) { return (uint32_t)((pt / C4 + i * (NP / C4)) * 4 + r4); };
@@ -1156,6 +1162,9 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
 
 int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hipStream_t stream) {
   if (int rc = check_prefill(p0.S, p0.H, head_dim, p0.M, precision)) return rc;
+  if (p0.group == 0 || p0.H % p0.group != 0)
+    return fail(STS_ERR_INVALID, "query heads %u not a multiple of the K/V group %u", p0.H,
+                p0.group);
   PrefillParams p = p0;
   p.wait_limit = wait_limit();
   if (int rc = device_error_word(&p.err)) return rc;

@@ -8,14 +8,16 @@
 namespace sts {
 
 // Query i (0 <= i < S) is window row len - S + i and attends window rows
-// 0..len-S+i; window row r of head h is slot (start + r) % M of
-// k + h*M*D.  q, out are [S][H][D].
+// 0..len-S+i; window row r of query head h is slot (start + r) % M of
+// k + (h / group)*M*D (group > 1: grouped-query attention, each K/V head
+// serving `group` consecutive query heads).  q, out are [S][H][D].
 struct PrefillParams {
   const float* q = nullptr;
   const float* k = nullptr;
   const float* v = nullptr;
   float* out = nullptr;
   uint32_t S = 0, H = 0, M = 0;
+  uint32_t group = 1;  // query heads per K/V head
   uint32_t start = 0, len = 0;
   float scale_log2 = 0.f;
   // Key-range split: up to nsplit workgroups share a (head, query tile); each

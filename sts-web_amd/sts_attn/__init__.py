@@ -55,7 +55,7 @@ class StsError(RuntimeError):
 class KvState(ctypes.Structure):
     _fields_ = [("offset", _u64), ("len", _u64), ("write_pos", _u64), ("max_len", _u64),
                 ("heads", _u64), ("head_dim", _u64), ("batch", _u64), ("allocated", ctypes.c_int32),
-                ("flags", ctypes.c_int32)]
+                ("flags", ctypes.c_int32), ("q_heads", _u64)]
 
 
 # name -> (restype, argtypes); the exported set of include/sts_attn.h.
@@ -78,6 +78,7 @@ SIGNATURES = {
     "sts_kv_create_ex": (_int, [_u64, _u64, _u64, _u32, ctypes.POINTER(_vp)]),
     "sts_kv_mirror": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
     "sts_kv_sync_mirror": (_int, [_vp, _vp]),
+    "sts_kv_set_query_heads": (_int, [_vp, _u64]),
     "sts_prefill_attention_bf16kv": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
                                             _u32, _f32, _vp]),
     "sts_kv_destroy": (_int, [_vp]),
@@ -303,13 +304,19 @@ class RoPE:
 class KVCache:
     """Ring-buffer KV cache in HBM, KVCache (model.rs:195-363)."""
 
-    def __init__(self, max_len: int, n_kv_heads: int, head_dim: int, bf16_mirror: bool = False):
+    def __init__(self, max_len: int, n_kv_heads: int, head_dim: int, bf16_mirror: bool = False,
+                 n_heads: Optional[int] = None):
+        """n_heads: query heads when they outnumber the K/V heads (grouped-query
+        attention, model.rs:766-783); q and out then have n_heads heads."""
         h = _vp()
         _check(load().sts_kv_create_ex(max_len, n_kv_heads, head_dim,
                                        KV_BF16_MIRROR if bf16_mirror else 0, ctypes.byref(h)))
         self._h = h
         self.n_kv_heads = n_kv_heads
+        self.n_heads = n_heads or n_kv_heads
         self.head_dim = head_dim
+        if self.n_heads != n_kv_heads:
+            _check(load().sts_kv_set_query_heads(h, self.n_heads))
 
     @property
     def handle(self):
@@ -436,8 +443,10 @@ class KVCache:
 class LayerCaches:
     """One KVCache per layer, LayerCaches (model.rs:365-411)."""
 
-    def __init__(self, n_layers: int, max_len: int, n_kv_heads: int, head_dim: int):
-        self.caches = [KVCache(max_len, n_kv_heads, head_dim) for _ in range(n_layers)]
+    def __init__(self, n_layers: int, max_len: int, n_kv_heads: int, head_dim: int,
+                 n_heads: Optional[int] = None):
+        self.caches = [KVCache(max_len, n_kv_heads, head_dim, n_heads=n_heads)
+                       for _ in range(n_layers)]
 
     def get_mut(self, layer: int) -> Optional[KVCache]:
         return self.caches[layer] if 0 <= layer < len(self.caches) else None

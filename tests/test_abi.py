@@ -42,7 +42,37 @@ def test_library_exports_every_declared_symbol():
     lib = sts_attn.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.sts_abi_version() == 2
+    assert lib.sts_abi_version() == 3
+    # The header's version macro agrees with the library's.
+    text = open(HEADER).read()
+    assert int(re.search(r"#define STS_ATTN_ABI_VERSION (\d+)", text).group(1)) == 3
+
+
+def test_kv_state_layout_matches_header():
+    """sts_kv_state field order and types as the header declares them."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct sts_kv_state \{(.*?)\} sts_kv_state;", text, re.S).group(1)
+    fields = re.findall(r"(u?int\d+_t)\s+(\w+);", body)
+    ctypes_of = {"uint64_t": ctypes.c_uint64, "int32_t": ctypes.c_int32}
+    assert [(n, ctypes_of[t]) for t, n in fields] == list(sts_attn.KvState._fields_)
+    assert ctypes.sizeof(sts_attn.KvState) == 72
+
+
+def test_query_heads_argument_errors():
+    """Grouped-query setter: a multiple of the K/V heads, at least them, at most
+    65535; a rejected call leaves the handle's query heads unchanged."""
+    lib = sts_attn.load()
+    c = sts_attn.KVCache(16, 4, 64)
+    s = lib.sts_kv_set_query_heads
+    assert "null" in _err(s(None, 8))
+    assert "multiple" in _err(s(c.handle, 6))
+    assert "multiple" in _err(s(c.handle, 2))
+    assert "multiple" in _err(s(c.handle, 4 * 65536))
+    assert c.state().q_heads == 4
+    assert s(c.handle, 12) == 0
+    assert c.state().q_heads == 12 and c.state().heads == 4
+    g = sts_attn.KVCache(16, 2, 128, n_heads=8)
+    assert (g.state().heads, g.state().q_heads) == (2, 8)
 
 
 def test_status_constants_match_header():

@@ -430,3 +430,27 @@ def test_decode_frame_equals_per_layer_shader_order():
         want = oracle.attention_ring_wgsl(qs[layer], kcs[layer], vcs[layer], starts[layer],
                                           lens[layer], 0.125)
         np.testing.assert_array_equal(got[layer], want)
+
+
+def test_gqa_expand_against_reference_op_sequence():
+    """orc_gqa_expand against model.rs:766-783's own operations restated with
+    torch on the CPU (unsqueeze at dim 2, repeat along it, reshape), a hand
+    example, and a planted interleaved (tiled) mapping that must differ."""
+    import torch
+    a = np.full((1, 2), 1.0, np.float32)
+    b = np.full((1, 2), 2.0, np.float32)
+    kv = np.stack([a, b])[None]                       # [B=1, nkv=2, S=1, D=2]
+    got = oracle.gqa_expand(kv, 2)
+    np.testing.assert_array_equal(got[0, :, 0, 0], [1.0, 1.0, 2.0, 2.0])
+    np.testing.assert_array_equal(oracle.gqa_expand(kv, 1), kv)
+    k = oracle.normal(77, (3, 4, 5, 8))               # [B, nkv, S, D]
+    for rep in (1, 2, 4):
+        t = torch.from_numpy(k)
+        B, nkv, S, D = t.shape
+        want = t.unsqueeze(2).repeat(1, 1, rep, 1, 1).reshape(B, nkv * rep, S, D).numpy()
+        np.testing.assert_array_equal(oracle.gqa_expand(k, rep), want)
+        if rep > 1:
+            tiled = np.tile(k, (1, rep, 1, 1))         # head h -> K/V head h % nkv: wrong
+            assert not np.array_equal(oracle.gqa_expand(k, rep), tiled)
+    # Without a batch axis (one stream's [nkv][M][D] cache).
+    np.testing.assert_array_equal(oracle.gqa_expand(k[1], 2), oracle.gqa_expand(k, 2)[1])
