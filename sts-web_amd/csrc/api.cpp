@@ -44,9 +44,12 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Any multiple of 4 up to 128 (shader_attention.wgsl:36 takes head_dim <= 128);
+// 64 and 128 have their own kernels, the others run padded ones.
 int check_head_dim(uint64_t d) {
-  if (d != 64 && d != 128) return fail(STS_ERR_INVALID, "head_dim %llu not supported (64 or 128)",
-                                       (unsigned long long)d);
+  if (d == 0 || d > 128 || d % 4 != 0)
+    return fail(STS_ERR_INVALID, "head_dim %llu not supported (a multiple of 4 up to 128)",
+                (unsigned long long)d);
   return STS_OK;
 }
 
@@ -293,6 +296,8 @@ int sts_prefill_attention_bf16kv(const float* q, const uint16_t* k16, const uint
   STS_CHECK(win_len <= max_len, "win_len %u > max_len %u", win_len, max_len);
   STS_CHECK(win_start < max_len, "win_start %u >= max_len %u", win_start, max_len);
   if (int rc = sts::check_prefill(seq, heads, head_dim, max_len, STS_PREC_BF16_MFMA)) return rc;
+  STS_CHECK(head_dim == 64 || head_dim == 128, "bf16 K/V rows need head_dim 64 or 128 (got %u)",
+            head_dim);
   STS_CHECK(aligned16(q) && aligned16(k16) && aligned16(v16) && aligned16(out),
             "pointers must be 16-byte aligned");
   STS_CHECK(std::isfinite(scale), "scale must be finite");

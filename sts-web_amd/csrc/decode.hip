@@ -96,7 +96,10 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-template <int D, int WAVES>
+// PAD: a head dim below D (a multiple of 4, p.head_dim) on the D-wide lane
+// layout: the lanes past it load zeros, so they add nothing to the scores or
+// the weighted sums, and store nothing.
+template <int D, int WAVES, bool PAD = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p) {
   constexpr int G = D / 4;
   constexpr int NG = 64 / G;
@@ -122,14 +125,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     const int32_t st = p.starts[b] % (int32_t)p.M;
     start = (uint32_t)(st < 0 ? st + (int32_t)p.M : st);
   } else {
-    len = p.len;
+    len = p.len + (PAD ? b * p.len_step : 0u);
     start = p.start;
   }
 
-  float* outp = p.out + b * p.out_bstride + (size_t)h * D;
+  const uint32_t dh = PAD ? p.head_dim : (uint32_t)D;  // the head dim in memory
+  const bool lane_ok = !PAD || (uint32_t)c * 4 < dh;   // this lane's 4 dims exist
+  float* outp = p.out + b * p.out_bstride + (size_t)h * dh;
   if (len == 0) {
     if (split == 0)
-      for (int t = tid; t < D; t += WAVES * 64) outp[t] = 0.f;
+      for (int t = tid; t < (int)dh; t += WAVES * 64) outp[t] = 0.f;
     return;
   }
   // This (stream, head) gets ceil(len / chunk) splits (at most nsplit_max);
@@ -140,15 +145,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   if (split >= nsplit) return;
   const uint32_t nunits = (len + RPI - 1) / RPI;
 
-  const size_t qoff = b * p.q_bstride + (size_t)h * D + c * 4;
+  const size_t qoff = b * p.q_bstride + (size_t)h * dh + c * 4;
   // q is rotated and scaled before the first K/V loads are issued: issuing
   // them first and waiting for q afterwards measured ~1 us slower per
   // config-2 launch (20.3 vs 19.25 us), on the same box.
-  float4 q4 = ld4(p.q + qoff);
+  float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (lane_ok) q4 = ld4(p.q + qoff);
   float2 rc = make_float2(0.f, 0.f), rs = make_float2(0.f, 0.f);
-  const bool rope = p.rope_cos != nullptr;
+  const bool rope = p.rope_cos != nullptr && lane_ok;
   if (rope) {
-    const size_t ro = (size_t)p.rope_pos * (D / 2) + c * 2;
+    const uint32_t pos = p.rope_pos + (PAD ? b * p.len_step : 0u);
+    const size_t ro = (size_t)pos * (dh / 2) + c * 2;
     rc = *reinterpret_cast<const float2*>(p.rope_cos + ro);
     rs = *reinterpret_cast<const float2*>(p.rope_sin + ro);
     q4 = rope4(q4, rc, rs);
@@ -165,7 +172,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // a row outside the window gets an offset past the resource and loads
   // zeros, so every load is issued unconditionally and the compiler's wait
   // counts see one fixed order of loads (no drain before each batch).
-  const uint32_t head_bytes = p.M * (uint32_t)(D * sizeof(float));
+  const uint32_t head_bytes = p.M * dh * (uint32_t)sizeof(float);
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(p.k) + kvoff, 0, (int)head_bytes, kBufferWord3);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -179,9 +186,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   // the wave whose unit holds it, which also use it from registers.
   float4 kn = make_float4(0.f, 0.f, 0.f, 0.f), vn = kn;
   if (append) {
-    const size_t knoff = b * (p.kn_bstride ? p.kn_bstride : p.q_bstride) + (size_t)kvh * D + c * 4;
-    kn = ld4(p.k_new + knoff);
-    vn = ld4(p.v_new + knoff);
+    const size_t knoff = b * (p.kn_bstride ? p.kn_bstride : p.q_bstride) + (size_t)kvh * dh + c * 4;
+    if (lane_ok) {
+      kn = ld4(p.k_new + knoff);
+      vn = ld4(p.v_new + knoff);
+    }
   }
 
   float m = -FLT_MAX;
@@ -196,7 +205,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       const uint32_t r = r0 + j * NG + g;
       uint32_t slot = start + r;
       slot = slot >= p.M ? slot - p.M : slot;
-      const uint32_t off = r < len ? slot * (uint32_t)(D * sizeof(float)) + c * 16 : 0x80000000u;
+      const uint32_t off =
+          r < len && lane_ok ? slot * (dh * (uint32_t)sizeof(float)) + c * 16 : 0x80000000u;
       kk[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, kNt));
       vv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, kNt));
     }
@@ -263,17 +273,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       if (rope) kn = rope4(kn, rc, rs);
       // Every query head of a K/V group uses the row from registers; the
       // group's first head stores it.
-      if (h == kvh * p.group) {
+      if (h == kvh * p.group && lane_ok) {
         uint32_t slot = start + new_row;
         slot = slot >= p.M ? slot - p.M : slot;
-        st4(p.k_wr + kvoff + (size_t)slot * D + c * 4, kn);
-        st4(p.v_wr + kvoff + (size_t)slot * D + c * 4, vn);
+        st4(p.k_wr + kvoff + (size_t)slot * dh + c * 4, kn);
+        st4(p.v_wr + kvoff + (size_t)slot * dh + c * 4, vn);
         if (p.k16_wr) {
           typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
           const bf16x4 kb = {(__bf16)kn.x, (__bf16)kn.y, (__bf16)kn.z, (__bf16)kn.w};
           const bf16x4 vb = {(__bf16)vn.x, (__bf16)vn.y, (__bf16)vn.z, (__bf16)vn.w};
-          *reinterpret_cast<bf16x4*>(p.k16_wr + kvoff + (size_t)slot * D + c * 4) = kb;
-          *reinterpret_cast<bf16x4*>(p.v16_wr + kvoff + (size_t)slot * D + c * 4) = vb;
+          *reinterpret_cast<bf16x4*>(p.k16_wr + kvoff + (size_t)slot * dh + c * 4) = kb;
+          *reinterpret_cast<bf16x4*>(p.v16_wr + kvoff + (size_t)slot * dh + c * 4) = vb;
         }
       }
     }
@@ -353,7 +363,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   }
 
   if (nsplit == 1) {
-    if (lane < C4)
+    if (lane < C4 && (!PAD || (uint32_t)col * 4 < dh))
       st4(outp + col * 4, make_float4(a4.x / l_t, a4.y / l_t, a4.z / l_t, a4.w / l_t));
     return;
   }
@@ -441,7 +451,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   o4.y += xor32(o4.y);
   o4.z += xor32(o4.z);
   o4.w += xor32(o4.w);
-  if (lane < C4) st4(outp + col * 4, make_float4(o4.x / l, o4.y / l, o4.z / l, o4.w / l));
+  if (lane < C4 && (!PAD || (uint32_t)col * 4 < dh))
+    st4(outp + col * 4, make_float4(o4.x / l, o4.y / l, o4.z / l, o4.w / l));
   if (lane == 0) atomicExch(ctr, 0u);
 }
 
@@ -493,9 +504,15 @@ DecodePlan plan_decode(uint64_t units, uint32_t max_rows) {
   return pl;
 }
 
+// The lane layout a head dim runs on: 64 or 128 (padded for the others).
+uint32_t padded_head_dim(uint32_t head_dim) { return head_dim <= 64 ? 64u : 128u; }
+
 int check_decode(const DecodeParams& p, uint32_t batch, uint32_t head_dim) {
-  if (head_dim != 64 && head_dim != 128)
-    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  if (head_dim == 0 || head_dim > 128 || head_dim % 4 != 0)
+    return fail(STS_ERR_INVALID, "head_dim %u not supported (a multiple of 4 up to 128)",
+                head_dim);
+  if (p.len_step && (p.lens || (head_dim == 64 || head_dim == 128)))
+    return fail(STS_ERR_INVALID, "per-stream window steps serve padded head dims only");
   if ((uint64_t)p.M * head_dim * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
   if (batch > 65535u || p.H > 65535u)
@@ -509,17 +526,30 @@ int launch_planned(DecodeParams p, const DecodePlan& pl, uint32_t batch, uint32_
                    hipStream_t stream) {
   p.chunk = pl.chunk;
   p.nsplit_max = pl.nsplit;
+  p.head_dim = head_dim;
   const dim3 grid(pl.nsplit, p.H, batch);
+  const bool one = pl.waves == 1;
+  const dim3 block(one ? 64 : 256);
   if (head_dim == 128) {
-    if (pl.waves == 1)
-      hipLaunchKernelGGL((decode_kernel<128, 1>), grid, dim3(64), 0, stream, p);
+    if (one)
+      hipLaunchKernelGGL((decode_kernel<128, 1>), grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<128, 4>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 4>), grid, block, 0, stream, p);
+  } else if (head_dim == 64) {
+    if (one)
+      hipLaunchKernelGGL((decode_kernel<64, 1>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_kernel<64, 4>), grid, block, 0, stream, p);
+  } else if (head_dim < 64) {
+    if (one)
+      hipLaunchKernelGGL((decode_kernel<64, 1, true>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_kernel<64, 4, true>), grid, block, 0, stream, p);
   } else {
-    if (pl.waves == 1)
-      hipLaunchKernelGGL((decode_kernel<64, 1>), grid, dim3(64), 0, stream, p);
+    if (one)
+      hipLaunchKernelGGL((decode_kernel<128, 1, true>), grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_kernel<64, 4>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, 4, true>), grid, block, 0, stream, p);
   }
   STS_HIP(hipGetLastError());
   return STS_OK;
@@ -578,7 +608,8 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   if (pl.nsplit > 1) {
     // Partials and arrival counters.
     Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)units * pl.nsplit * (head_dim + 4), units, &ws);
+    const int rc = get_workspace(stream, (size_t)units * pl.nsplit * (padded_head_dim(head_dim) + 4),
+                                 units, &ws);
     if (rc != STS_OK) return rc;
     p.part = ws->part;
     p.counters = ws->counters;
@@ -593,7 +624,7 @@ int launch_decode_noalloc(DecodeParams p, uint32_t batch, uint32_t head_dim, uin
   if (int rc = check_decode(p, batch, head_dim)) return rc;
   const DecodePlan pl = plan_decode(units, max_rows);
   if (pl.nsplit > 1) {
-    const uint64_t need = units * pl.nsplit * (head_dim + 4);
+    const uint64_t need = units * pl.nsplit * (padded_head_dim(head_dim) + 4);
     if (need > kScratchPartFloats || units > kScratchCounters)
       return fail(STS_ERR_INVALID,
                   "this launch needs %llu floats of split records and %llu counters; the "

@@ -41,6 +41,15 @@ struct DecodeParams {
   uint32_t nsplit_max = 1; // grid x
   float* part = nullptr;   // [B][H][nsplit_max][D+4] partials (nsplit > 1 only)
   uint32_t* counters = nullptr;  // [B][H] arrival counters, zero between calls
+  // Last, so that the fields the kernel's prologue needs keep their shared
+  // 16-byte kernel-argument loads.  The head dim in memory, set by the
+  // launcher (64 and 128 run their own layouts; other multiples of 4 up to
+  // 128 a padded one).
+  uint32_t head_dim = 0;
+  // Padded head dims only, with lens == null: stream b's window has
+  // len + b * len_step rows and its RoPE position is rope_pos + b * len_step
+  // (the queries of a causal chunk as streams over one cache: kv_bstride 0).
+  uint32_t len_step = 0;
 };
 
 // scale * log2(e), the factor the decode and prefill kernels fold into q.

@@ -31,6 +31,7 @@
 
 #include "coherent.hpp"
 #include "common.hpp"
+#include "decode.hpp"
 #include "errors.hpp"
 #include "lane.hpp"
 #include "prefill.hpp"
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   const int g = lane >> 4;
   const int l16 = lane & 15;
   const uint32_t h = blockIdx.x;
-  const uint32_t kvh = p.group == 1 ? h : h / p.group;  // its K/V head
+  const uint32_t kvh = p.group_magic ? __umulhi(h, p.group_magic) : h;  // its K/V head
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   const uint32_t qt = nqt - 1 - blockIdx.y;
   const uint32_t split = blockIdx.z;
@@ -604,7 +605,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t h = blockIdx.x;
-  const uint32_t kvh = p.group == 1 ? h : h / p.group;  // its K/V head
+  const uint32_t kvh = p.group_magic ? __umulhi(h, p.group_magic) : h;  // its K/V head
   const uint32_t nqt = (p.S + QT - 1) / QT;
   const uint32_t qt = nqt - 1 - blockIdx.y;  // heaviest tiles first
   const uint32_t base_w = p.len - p.S;
@@ -1148,8 +1149,9 @@ int launch_f32(const PrefillParams& p, hipStream_t stream) {
 
 int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_len,
                   int precision) {
-  if (head_dim != 128 && head_dim != 64)
-    return fail(STS_ERR_INVALID, "head_dim %u not supported (64 or 128)", head_dim);
+  if (head_dim == 0 || head_dim > 128 || head_dim % 4 != 0)
+    return fail(STS_ERR_INVALID, "head_dim %u not supported (a multiple of 4 up to 128)",
+                head_dim);
   if (precision != STS_PREC_F32 && precision != STS_PREC_BF16_MFMA &&
       precision != STS_PREC_F32_SPLIT_BF16)
     return fail(STS_ERR_INVALID, "precision %d unknown", precision);
@@ -1160,12 +1162,47 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
   return STS_OK;
 }
 
+// Head dims other than 64 and 128 (multiples of 4 up to 128, which the
+// reference's shader also takes, shader_attention.wgsl:36): query i of the
+// chunk is a decode over window rows 0..len-S+i, exactly the S sequential
+// decodes the reference's prefill stands for, run as one launch of the
+// padded decode kernel with the queries as streams over the shared cache.
+// Always f32, whatever precision was asked for.
+static int launch_prefill_by_decode(const PrefillParams& p, uint32_t head_dim,
+                                    hipStream_t stream) {
+  if (!p.k || !p.v) return fail(STS_ERR_INVALID, "head_dim %u needs the f32 caches", head_dim);
+  DecodeParams d;
+  d.q = p.q;
+  d.k = p.k;
+  d.v = p.v;
+  d.out = p.out;
+  d.H = p.H;
+  d.M = p.M;
+  d.group = p.group;
+  d.q_bstride = (uint64_t)p.H * head_dim;
+  d.out_bstride = (uint64_t)p.H * head_dim;
+  d.kv_bstride = 0;
+  d.kv_hstride = (uint64_t)p.M * head_dim;
+  d.len = p.len - p.S + 1;
+  d.len_step = 1;
+  d.start = p.start;
+  d.scale_log2 = p.scale_log2;
+  if (p.rope_cos) {
+    d.rope_cos = p.rope_cos;
+    d.rope_sin = p.rope_sin;
+    d.rope_pos = p.rope_pos0;
+  }
+  return launch_decode(d, p.S, head_dim, p.len, stream);
+}
+
 int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hipStream_t stream) {
   if (int rc = check_prefill(p0.S, p0.H, head_dim, p0.M, precision)) return rc;
   if (p0.group == 0 || p0.H % p0.group != 0)
     return fail(STS_ERR_INVALID, "query heads %u not a multiple of the K/V group %u", p0.H,
                 p0.group);
+  if (head_dim != 64 && head_dim != 128) return launch_prefill_by_decode(p0, head_dim, stream);
   PrefillParams p = p0;
+  p.group_magic = p.group > 1 ? (uint32_t)(((1ull << 32) + p.group - 1) / p.group) : 0u;
   p.wait_limit = wait_limit();
   if (int rc = device_error_word(&p.err)) return rc;
   const bool d128 = head_dim == 128;

@@ -17,7 +17,6 @@ struct PrefillParams {
   const float* v = nullptr;
   float* out = nullptr;
   uint32_t S = 0, H = 0, M = 0;
-  uint32_t group = 1;  // query heads per K/V head
   uint32_t start = 0, len = 0;
   float scale_log2 = 0.f;
   // Key-range split: up to nsplit workgroups share a (head, query tile); each
@@ -39,6 +38,12 @@ struct PrefillParams {
   // kernel reads them instead of k / v.
   const void* k16 = nullptr;
   const void* v16 = nullptr;
+  // Query heads per K/V head (last, so the other fields keep their
+  // kernel-argument load groups).  The kernels take the K/V head of query
+  // head h as umulhi(h, group_magic) = h / group (exact for h, group < 2^16),
+  // group_magic = ceil(2^32 / group), set by launch_prefill; 0 for group 1.
+  uint32_t group = 1;
+  uint32_t group_magic = 0;
 };
 
 // Checks everything launch_prefill would reject for these sizes, without

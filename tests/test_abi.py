@@ -101,7 +101,10 @@ def test_fused_attention_argument_errors():
     lib = sts_attn.load()
     f = lib.sts_fused_attention
     assert "null" in _err(f(None, FAKE, FAKE, FAKE, 32, 128, 10, 0.1, 1280, None))
-    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 100, 10, 0.1, 1000, None))
+    # Any multiple of 4 up to 128 is taken (the shader's limit); others are not.
+    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 102, 10, 0.1, 1020, None))
+    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 0, 10, 0.1, 0, None))
+    assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 132, 10, 0.1, 1320, None))
     assert "head_dim" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 256, 10, 0.1, 2560, None))
     assert "seq_len" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 128, 0, 0.1, 1280, None))
     assert "stride" in _err(f(FAKE, FAKE, FAKE, FAKE, 32, 128, 10, 0.1, 128, None))
@@ -120,7 +123,7 @@ def test_decode_ring_and_depformer_argument_errors():
     lib = sts_attn.load()
     assert "null" in _err(lib.sts_decode_ring(FAKE, FAKE, FAKE, FAKE, None, FAKE, 4, 32, 128,
                                               3000, 0.1, None))
-    assert "head_dim" in _err(lib.sts_decode_ring(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 96,
+    assert "head_dim" in _err(lib.sts_decode_ring(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 32, 98,
                                                   3000, 0.1, None))
     assert "step" in _err(lib.sts_depformer_step(FAKE, FAKE, FAKE, 3072, FAKE, FAKE, FAKE, 64,
                                                  16, 64, 9, 9, 0.125, None))
@@ -159,10 +162,19 @@ def test_kv_prefill_rejects_before_any_device_work():
         assert (s.offset, s.len, s.write_pos, s.allocated) == (0, 0, 0, 0)
 
 
+def test_bf16kv_prefill_needs_its_head_dims():
+    """The bf16-K/V prefill has no padded form: head dims other than 64 and 128
+    are refused before any device work."""
+    lib = sts_attn.load()
+    assert "bf16 K/V" in _err(lib.sts_prefill_attention_bf16kv(FAKE, FAKE, FAKE, FAKE, 4, 2, 96,
+                                                                100, 0, 50, 0.1, None))
+
+
 def test_kv_handle_argument_errors():
     lib = sts_attn.load()
     h = ctypes.c_void_p()
-    assert "head_dim" in _err(lib.sts_kv_create(3000, 32, 100, ctypes.byref(h)))
+    assert "head_dim" in _err(lib.sts_kv_create(3000, 32, 102, ctypes.byref(h)))
+    assert "head_dim" in _err(lib.sts_kv_create(3000, 32, 192, ctypes.byref(h)))
     assert "max_len" in _err(lib.sts_kv_create(0, 32, 128, ctypes.byref(h)))
     assert "null" in _err(lib.sts_kv_advance(None, 1))
     c = sts_attn.KVCache(8, 2, 64)
@@ -176,7 +188,7 @@ def test_kv_handle_argument_errors():
 def test_rope_argument_errors():
     lib = sts_attn.load()
     h = ctypes.c_void_p()
-    assert "head_dim" in _err(lib.sts_rope_create(100, 3000, 1e4, ctypes.byref(h)))
+    assert "head_dim" in _err(lib.sts_rope_create(102, 3000, 1e4, ctypes.byref(h)))
     assert "theta" in _err(lib.sts_rope_create(128, 3000, -1.0, ctypes.byref(h)))
     assert "null" in _err(lib.sts_rope_apply(None, FAKE, 1, 1, 32, 0, None))
 
