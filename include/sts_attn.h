@@ -24,10 +24,14 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
  *     device work is enqueued asynchronously on it; nothing blocks the host
  *     except the one-time allocation of library workspace (see below).
- *   - head_dim must be 64 or 128 (the two head sizes of the model: temporal
- *     4096/32, depformer 1024/16; lib.rs:128-140).  The reference shader
- *     silently overflows for head_dim > 128 (shader_attention.wgsl:66); here it
- *     is an error.
+ *   - head_dim is a multiple of 4 up to 128.  The model's two head sizes
+ *     (temporal 4096/32 = 128, depformer 1024/16 = 64; lib.rs:128-140) run
+ *     their own kernels; the others run a padded decode kernel, and their
+ *     prefill is the chunk's queries as decodes over their causal windows, in
+ *     f32 whatever precision is asked (the bf16-K/V prefill takes 64 and 128
+ *     only).  The reference shader takes any head_dim up to 128 and silently
+ *     overflows beyond (shader_attention.wgsl:36, :66); here that is an
+ *     error, and so is a head_dim that is not a multiple of 4.
  *   - Attention entry points use a per-(device, stream) workspace owned by the
  *     library for split-KV partial results.  It is allocated (hipMalloc) on the
  *     first call on a stream that needs it and grown when a larger launch needs
