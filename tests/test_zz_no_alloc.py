@@ -71,7 +71,7 @@ def test_noalloc_refuses_launches_beyond_the_array():
     # Argument checks are those of sts_decode_ring.
     assert fn(None, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 32, 128, 3000, 0.1, None) == \
         sts_attn.STS_ERR_INVALID
-    assert fn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 32, 100, 3000, 0.1, None) == \
+    assert fn(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 32, 102, 3000, 0.1, None) == \
         sts_attn.STS_ERR_INVALID
     assert ctypes.c_int(fn(FAKE, FAKE, FAKE, FAKE + 4, FAKE, FAKE, 1, 32, 128, 3000, 0.1,
                            None)).value == sts_attn.STS_ERR_INVALID
