@@ -1157,6 +1157,9 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
     return fail(STS_ERR_INVALID, "precision %d unknown", precision);
   if (heads < 1 || heads > 65535u) return fail(STS_ERR_INVALID, "heads %u out of 1..65535", heads);
   if ((seq + 63u) / 64u > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", seq);
+  // Other head dims run the queries as streams of one decode launch.
+  if (head_dim != 64 && head_dim != 128 && seq > 65535u)
+    return fail(STS_ERR_INVALID, "seq %u too long for one launch at head_dim %u", seq, head_dim);
   if ((uint64_t)max_len * head_dim * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", max_len);
   return STS_OK;

@@ -170,6 +170,19 @@ def test_bf16kv_prefill_needs_its_head_dims():
                                                                 100, 0, 50, 0.1, None))
 
 
+def test_padded_head_dim_prefill_length_checked_first():
+    """At head dims other than 64/128 a chunk runs as one decode launch with
+    the queries as streams (at most 65535): a longer chunk is refused before
+    anything is appended (fake pointers, never dereferenced)."""
+    lib = sts_attn.load()
+    c = sts_attn.KVCache(100000, 2, 96)
+    rc = lib.sts_kv_prefill(c.handle, None, FAKE, FAKE, FAKE, FAKE, 70000, 0.1,
+                            sts_attn.PREC_F32, None)
+    assert "too long" in _err(rc)
+    s = c.state()
+    assert (s.offset, s.len, s.allocated) == (0, 0, 0)
+
+
 def test_kv_handle_argument_errors():
     lib = sts_attn.load()
     h = ctypes.c_void_p()
