@@ -441,9 +441,12 @@ int sts_q4k_dequant(const uint8_t* weights, float* out, uint32_t k, uint32_t n, 
  * x * (1/sqrt(mean(x^2) + norm_eps)) * norm_alpha (the RMSNorm that precedes
  * every projection of the depformer, depth_engine.rs:1069-1095, 1262-1282,
  * fused; its sum of squares is taken in this kernel's order, not the
- * shader's).  k must be a multiple of 256 in 256..4096; x rows, norm_alpha
- * and weights 16-byte aligned; ldx, ldy, ldr are row strides in floats (ldx a
- * multiple of 4).
+ * shader's).  k must be a multiple of 256 in 256..16384; above 4096 (the
+ * temporal FFN's linear_out, k = 11264) the product runs as slices of 4096
+ * summed in slice order by a second kernel, through the stream's library
+ * workspace (see the workspace rules above), without norm_alpha or swiglu.
+ * x rows, norm_alpha and weights 16-byte aligned; ldx, ldy, ldr are row
+ * strides in floats (ldx a multiple of 4).
  */
 int sts_q4k_gemm(const uint8_t* weights, const float* x, uint64_t ldx, const float* norm_alpha,
                  float norm_eps, const float* residual, uint64_t ldr, float* y, uint64_t ldy,

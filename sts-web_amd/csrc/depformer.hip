@@ -66,7 +66,7 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
   float* Y = p.y + z * p.y_zstride;
   const uint32_t nout = SWIGLU ? p.swiglu_f : p.N;
   const uint32_t ntiles = (nout + 15) / 16;
-  const size_t row_bytes = (size_t)KB * kQ4kBlockBytes;
+  const size_t row_bytes = (size_t)(p.w_row_blocks ? p.w_row_blocks : KB) * kQ4kBlockBytes;
 
   // Rows past the end (and tiles past the last) re-read valid rows; their
   // outputs are not stored.
@@ -493,11 +493,57 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   }
 }
 
+// y[m][n] = sum over the slices s of part[s][m][n] in slice order, plus
+// res[m][n]: the split-K sum of launch_q4k_gemm.
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part,
+                                                         uint32_t nsl, uint32_t M, uint32_t N,
+                                                         const float* __restrict__ res,
+                                                         uint64_t ldr, float* __restrict__ y,
+                                                         uint64_t ldy) {
+#pragma clang fp contract(off)
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)M * N) return;
+  const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+  float v = part[i];
+  for (uint32_t s = 1; s < nsl; ++s) v += part[(uint64_t)s * M * N + i];
+  if (res) v += res[(size_t)m * ldr + n];
+  y[(size_t)m * ldy + n] = v;
+}
+
 }  // namespace
 
 int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
+  if (p.K > 16 * kQ4kBlockWeights && p.K % kQ4kBlockWeights == 0 && p.K <= 64 * kQ4kBlockWeights) {
+    // Split K: slices of up to 16 super-blocks into a workspace, then the sum.
+    if (p.Z != 1 || p.swiglu_f || p.norm_alpha)
+      return fail(STS_ERR_INVALID, "GEMM with K = %u > 4096 takes no SwiGLU, RMSNorm or Z > 1",
+                  p.K);
+    if (p.M == 0 || p.N == 0) return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u", p.M, p.N);
+    const uint32_t KB = p.K / kQ4kBlockWeights;
+    const uint32_t nsl = (KB + 15) / 16;
+    const size_t mn = (size_t)p.M * p.N;
+    Workspace* ws = nullptr;
+    if (int rc = get_workspace(stream, nsl * mn, 0, &ws)) return rc;
+    for (uint32_t sl = 0; sl < nsl; ++sl) {
+      const uint32_t kb0 = sl * 16, kbs = std::min(16u, KB - kb0);
+      Q4kGemmParams q = p;
+      q.w[0] = p.w[0] + (size_t)kb0 * kQ4kBlockBytes;
+      q.x = p.x + (size_t)kb0 * kQ4kBlockWeights;
+      q.K = kbs * kQ4kBlockWeights;
+      q.w_row_blocks = KB;
+      q.res = nullptr;
+      q.y = ws->part + sl * mn;
+      q.ldy = p.N;
+      if (int rc = launch_q4k_gemm(q, stream)) return rc;
+    }
+    const uint64_t blocks = (mn + 255) / 256;
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                       ws->part, nsl, p.M, p.N, p.res, p.ldr, p.y, p.ldy);
+    STS_HIP(hipGetLastError());
+    return STS_OK;
+  }
   if (p.K % kQ4kBlockWeights != 0 || p.K == 0 || p.K > 16 * kQ4kBlockWeights)
-    return fail(STS_ERR_INVALID, "GEMM K = %u must be a multiple of 256 in 256..4096", p.K);
+    return fail(STS_ERR_INVALID, "GEMM K = %u must be a multiple of 256 in 256..16384", p.K);
   if (p.M == 0 || p.N == 0 || p.Z == 0 || p.Z > (uint32_t)kGemmMaxZ)
     return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u Z=%u", p.M, p.N, p.Z);
   if (p.swiglu_f && (p.swiglu_f * 2 != p.N))

@@ -31,7 +31,14 @@ struct Q4kGemmParams {
   // formula; the sum of squares is taken in this kernel's order).
   const float* norm_alpha = nullptr;
   float norm_eps = 0.f;
+  // Super-blocks per weight row when the launch covers only part of K (a
+  // split-K slice of a wider matrix); 0: K / 256.
+  uint32_t w_row_blocks = 0;
 };
+// K above 4096 (no RMSNorm or SwiGLU, Z = 1) runs as ceil(K / 4096) slices
+// into a stream workspace, summed in slice order by a second kernel that also
+// adds the residual: deterministic, and refused while the stream is being
+// captured if the workspace has to grow.
 int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream);
 
 // out[b][i] = x[b][i] * (1 / sqrt(sum x^2 / D + eps)) * alpha[i] in the

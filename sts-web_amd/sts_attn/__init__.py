@@ -525,7 +525,7 @@ def softmax_scale(head_dim: int) -> float:
 
 Q4K_BLOCK_BYTES = 144
 QK_K = 256
-GEMM_MAX_K = 4096  # sts_q4k_gemm's largest k; larger k goes through sts_q4k_matvec
+GEMM_MAX_K = 16384  # sts_q4k_gemm's largest k (above 4096 as summed slices of 4096)
 
 
 class Q4KTensor:
@@ -568,8 +568,8 @@ def q4k_matmul(input: torch.Tensor, weights: Q4KTensor, residual: Optional[torch
     """q4k_matmul / q4k_matmul_with_residual (gguf.rs:808-905): input
     [B, M, K] (or [B, K]) -> [B, M, N] = input @ W^T (+ residual).  M = 1 runs
     the matvec (the reference's single-token path), M > 1 the GEMM (its
-    prefill path) for K <= 4096 and the batched matvec (B*M rows) for larger K
-    (the temporal FFN's linear_out, K = 11264)."""
+    prefill path; K above 4096, the temporal FFN's linear_out at 11264, as
+    summed slices)."""
     n, k = weights.shape()
     if input.shape[-1] != k:
         raise StsError(STS_ERR_INVALID,

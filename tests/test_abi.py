@@ -289,6 +289,11 @@ def test_depformer_chain_argument_errors():
                                                       3072, 64, 1000, 3072, 0, None))
     assert "SwiGLU" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, None, 0.0, FAKE, 5632, FAKE, 2816,
                                              64, 1024, 5632, 1, None))
+    # Above k = 4096 (summed slices) no fused RMSNorm; beyond 16384 nothing.
+    assert "RMSNorm" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 11264, FAKE, 1e-5, None, 0, FAKE, 4096,
+                                              64, 11264, 4096, 0, None))
+    assert "multiple of 256" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 16640, None, 0.0, None, 0, FAKE,
+                                                      4096, 64, 16640, 4096, 0, None))
     assert "strides" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 512, None, 0.0, None, 0, FAKE, 3072, 64,
                                               1024, 3072, 0, None))
     assert "norm_eps" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, FAKE, -1.0, None, 0, FAKE, 3072,

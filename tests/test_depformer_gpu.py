@@ -68,7 +68,9 @@ def test_embed_add_bit_exact(gpu):
 @pytest.mark.parametrize("M,N,K,res", [(64, 3072, 1024, False), (64, 1024, 1024, True),
                                        (64, 1024, 2816, True), (64, 2048, 1024, False),
                                        (3, 1024, 4096, False), (17, 100, 512, True),
-                                       (1, 16, 256, False), (130, 48, 768, False)])
+                                       (1, 16, 256, False), (130, 48, 768, False),
+                                       (17, 300, 11264, True), (64, 1024, 8192, False),
+                                       (40, 64, 4352, True)])
 def test_q4k_gemm_against_oracle(gpu, M, N, K, res):
     print(f"q4k gemm M={M} N={N} K={K} res={res}", flush=True)
     blocks = oracle.q4k_random_blocks(M + N + K, N, K)

@@ -134,9 +134,9 @@ def test_matvec_argument_errors(gpu):
                                                   (300, 1024, 1, 7, True)])
 def test_matmul_many_rows(gpu, N, K, B, Mrows, residual):
     """q4k_matmul with M > 1 (the reference's prefill route, gguf.rs:810-897):
-    K <= 4096 runs the GEMM, larger K (the temporal FFN's linear_out, K = 11264)
-    the batched matvec over B*M rows; both within the f32 bound of the f64
-    product, with and without the residual (gguf.rs:899-905)."""
+    the GEMM, K above 4096 (the temporal FFN's linear_out, K = 11264) as summed
+    slices of 4096; within the f32 bound of the f64 product, with and without
+    the residual (gguf.rs:899-905)."""
     blocks = oracle.q4k_random_blocks(N + K + Mrows, N, K)
     w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
     x = oracle.normal(N + 3 * Mrows, (B, Mrows, K))
