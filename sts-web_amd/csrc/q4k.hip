@@ -15,11 +15,21 @@
 //     d1 * sum(q_lo * x_lo) - m1 * sum(x_lo) + d2 * sum(q_hi * x_hi) - m2 * sum(x_hi)
 // with the two sums of x computed once.  Per row a lane loads 48 bytes; the
 // lanes of a wave together read the row as one contiguous stream (2304
-// bytes at K = 4096).  Rows are dealt round-robin to the row groups of the
-// grid, U rows per group in flight at a time.  The regrouping changes the
-// rounding of the sum (tolerance-checked against the shader-order oracle),
-// not the weights: the dequantisation kernel below reproduces the shader's
-// f32 weights bit for bit.
+// bytes at K = 4096).  The regrouping changes the rounding of the sum
+// (tolerance-checked against the shader-order oracle), not the weights: the
+// dequantisation kernel below reproduces the shader's f32 weights bit for
+// bit.
+//
+// K <= 4096 (one wave per row): wave w of the W waves of the grid owns rows
+// w, w + W, ..., at most 12 of them, with two rows in flight: row j + 2 is
+// requested as soon as row j is reduced, and the first two before x is
+// staged.  Eight waves per CU.  Measured against the same kernel with more
+// rows in flight (three to all twelve, or four waves per CU): two rows and
+// eight waves is the fastest for every projection shape; with more requests
+// in flight the rows come back in an order that leaves waves waiting on
+// their first row.
+// K > 4096: KP waves share a row and combine through LDS; rows are dealt
+// round-robin to the row groups of the grid, two steps of U rows in flight.
 //
 // HBM-bound: 0.5625 bytes and 2 flops per weight (x and y are negligible).
 #include <algorithm>
@@ -81,8 +91,9 @@ __device__ __forceinline__ float wave_sum(float x) {
   return sum_xor32(sum_xor16(x));
 }
 
-// KP waves share a row (slots 64*kp + lane), G row groups per workgroup, U
-// rows per group per step, two steps in flight.  grid.y = batch.
+// K > 4096: KP waves share a row (slots 64*kp + lane) and combine through
+// LDS, G row groups per workgroup, U rows per group per step, two steps in
+// flight.  grid.y = batch.
 template <int KP, int G, int U>
 __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams p) {
   const int lane = threadIdx.x & 63;
@@ -97,7 +108,7 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
   const uint32_t blk = has ? s >> 2 : 0u, it = has ? s & 3u : 0u;
   const uint32_t b = blockIdx.y;
 
-  [[maybe_unused]] __shared__ float red[G][U][KP];
+  __shared__ float red[G][U][KP];
   const size_t row_bytes = (size_t)nb * kQ4kBlockBytes;
   const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
   const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
@@ -156,36 +167,22 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
     for (int u = 0; u < U; ++u)
       acc[u] = wave_sum(slot_dot(r.hd[u], r.qa[u], r.qb[u], 2 * it, xv, sxl, sxh));
     const uint32_t r0 = base + grp * U;
-    if constexpr (KP == 1) {
-      if (lane == 0) {
+    if (lane == 0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const uint32_t row = r0 + u;
-          if (row < p.N) {
-            float v = acc[u];
-            if (p.res) v += p.res[(size_t)b * p.N + row];
-            p.y[(size_t)b * p.N + row] = v;
-          }
-        }
-      }
-    } else {
-      if (lane == 0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) red[grp][u][kp] = acc[u];
-      }
-      __syncthreads();
-      if (kp == 0 && lane < U) {
-        const uint32_t row = r0 + lane;
-        if (row < p.N) {
-          float v = red[grp][lane][0];
-#pragma unroll
-          for (int k = 1; k < KP; ++k) v += red[grp][lane][k];
-          if (p.res) v += p.res[(size_t)b * p.N + row];
-          p.y[(size_t)b * p.N + row] = v;
-        }
-      }
-      __syncthreads();
+      for (int u = 0; u < U; ++u) red[grp][u][kp] = acc[u];
     }
+    __syncthreads();
+    if (kp == 0 && lane < U) {
+      const uint32_t row = r0 + lane;
+      if (row < p.N) {
+        float v = red[grp][lane][0];
+#pragma unroll
+        for (int k = 1; k < KP; ++k) v += red[grp][lane][k];
+        if (p.res) v += p.res[(size_t)b * p.N + row];
+        p.y[(size_t)b * p.N + row] = v;
+      }
+    }
+    __syncthreads();
   };
 
   // Two steps in flight: while one set of rows is reduced, the next loads.
@@ -196,6 +193,98 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
     finish(ra, base);
     load(ra, base + 2 * stride);
     if (base + stride < p.N) finish(rb, base + stride);
+  }
+}
+
+// K <= 4096: wave w owns rows w + j*W (j < R), two of them in flight.
+constexpr int kRowsInFlight = 2;
+
+template <int R>
+__global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t wpb = blockDim.x >> 6;
+  const uint32_t W = gridDim.x * wpb;
+  const uint32_t w = blockIdx.x * wpb + (threadIdx.x >> 6);
+  const uint32_t nb = p.K / kQ4kBlockWeights;
+  const uint32_t s = lane;  // this lane's slot
+  const bool has = s < 4u * nb;
+  // A lane without a slot reads slot 0 (valid memory) and contributes zero:
+  // its x values and their sums are zero.
+  const uint32_t blk = has ? s >> 2 : 0u, it = has ? s & 3u : 0u;
+  const uint32_t b = blockIdx.y;
+  const size_t row_bytes = (size_t)nb * kQ4kBlockBytes;
+  const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
+  const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
+
+  // x (at most 4096 floats, 1024 float4) is requested first, then the first
+  // rows, so that waiting for x does not wait for the weights.  The
+  // workgroup stages x in LDS, slot c at row c of pitch 68 floats (the 16
+  // lanes of a read phase then hit distinct banks), and each lane copies its
+  // slot into registers.
+  extern __shared__ __align__(16) float xs[];  // [K/64][68]
+  const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
+  const uint32_t n4 = p.K / 4;
+  const uint32_t i0 = threadIdx.x, i1 = i0 + blockDim.x, i2 = i1 + blockDim.x,
+                 i3 = i2 + blockDim.x;
+  const float4 x0 = xb[i0 < n4 ? i0 : 0u], x1 = xb[i1 < n4 ? i1 : 0u],
+               x2 = xb[i2 < n4 ? i2 : 0u], x3 = xb[i3 < n4 ? i3 : 0u];
+  // Keeps the x loads ahead of the weight loads in the issue order.
+  __builtin_amdgcn_sched_barrier(0);
+
+  u32x4 hd[R], qa[R], qb[R];
+  auto load = [&](int j) {
+    // Rows past the end re-read row N-1 and are not stored.
+    const size_t off = (size_t)min(w + j * W, p.N - 1) * row_bytes;
+    hd[j] = ld16(whead + off);
+    qa[j] = ld16_stream(wslot + off);
+    qb[j] = ld16_stream(wslot + off + 16);
+  };
+  constexpr int D = kRowsInFlight < R ? kRowsInFlight : R;
+#pragma unroll
+  for (int j = 0; j < D; ++j) load(j);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](uint32_t i, const float4& v) {
+    if (i < n4) *reinterpret_cast<float4*>(&xs[(i >> 4) * 68 + 4 * (i & 15)]) = v;
+  };
+  stage(i0, x0);
+  stage(i1, x1);
+  stage(i2, x2);
+  stage(i3, x3);
+  __syncthreads();
+  float xv[64];
+  const uint32_t xs0 = has ? s * 68 : 0u;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float4 t = *reinterpret_cast<const float4*>(&xs[xs0 + 4 * j]);
+    xv[4 * j] = has ? t.x : 0.f;
+    xv[4 * j + 1] = has ? t.y : 0.f;
+    xv[4 * j + 2] = has ? t.z : 0.f;
+    xv[4 * j + 3] = has ? t.w : 0.f;
+  }
+  float sxl = 0.f, sxh = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    sxl += xv[j];
+    sxh += xv[32 + j];
+  }
+
+  float acc[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    acc[j] = wave_sum(slot_dot(hd[j], qa[j], qb[j], 2 * it, xv, sxl, sxh));
+    if (j + D < R) load(j + D);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const uint32_t row = w + j * W;
+      if (row < p.N) {
+        float v = acc[j];
+        if (p.res) v += p.res[(size_t)b * p.N + row];
+        p.y[(size_t)b * p.N + row] = v;
+      }
+    }
   }
 }
 
@@ -239,14 +328,13 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
 
 template <int KP>
 int launch_kp(const Q4kParams& p, hipStream_t stream) {
-  constexpr int G = KP == 1 ? 4 : (KP == 2 ? 2 : 1);
+  static_assert(KP > 1, "K <= 4096 runs q4k_matvec_rows_kernel");
+  constexpr int G = KP == 2 ? 2 : 1;
   constexpr int U = 2;
-  // waves_per_cu waves per CU walking the rows; each workgroup reads x once
-  // into LDS.  Measured per shape: 4 per CU for the attention projections
-  // (in_proj 10.5 vs 11.6 us, out_proj 6.7 vs 7.7 us with 8), 8 for the long
-  // matrices and the rows split over several waves (FFN linear_in [22528,
-  // 4096] 14.2 vs 15.7 us, linear_out [4096, 11264] 12.7 vs 14.1 us).
-  const uint32_t waves_per_cu = (KP > 1 || p.N >= 16384) ? 8 : 4;
+  // Eight waves per CU walking the rows; each workgroup reads x once into
+  // LDS.  Measured for FFN linear_out [4096, 11264]: 12.7 us against 14.1
+  // with four.
+  const uint32_t waves_per_cu = 8;
   const uint32_t cus = (uint32_t)device_cu_count();
   const uint32_t steps = (p.N + G * U - 1) / (G * U);
   const uint32_t wgs = std::max(1u, std::min(steps, cus * waves_per_cu / (KP * G)));
@@ -259,9 +347,39 @@ int launch_kp(const Q4kParams& p, hipStream_t stream) {
 
 }  // namespace
 
+template <int R>
+int launch_rows(const Q4kParams& p, uint32_t wgs, hipStream_t stream) {
+  const size_t lds = (size_t)(p.K / 64) * 68 * sizeof(float);
+  hipLaunchKernelGGL((q4k_matvec_rows_kernel<R>), dim3(wgs, p.B), dim3(256), lds, stream, p);
+  STS_HIP(hipGetLastError());
+  return STS_OK;
+}
+
+// K <= 4096: eight waves per CU, or as many more as keep each wave at 12
+// rows or fewer; R = rows per wave.
+int launch_rows_any(const Q4kParams& p, hipStream_t stream) {
+  const uint32_t cus = (uint32_t)device_cu_count();
+  const uint32_t wgs = (std::max(8u * cus, (p.N + 11) / 12) + 3) / 4;
+  const uint32_t r = (p.N + 4 * wgs - 1) / (4 * wgs);
+  switch (r) {
+    case 1: return launch_rows<1>(p, wgs, stream);
+    case 2: return launch_rows<2>(p, wgs, stream);
+    case 3: return launch_rows<3>(p, wgs, stream);
+    case 4: return launch_rows<4>(p, wgs, stream);
+    case 5: return launch_rows<5>(p, wgs, stream);
+    case 6: return launch_rows<6>(p, wgs, stream);
+    case 7: return launch_rows<7>(p, wgs, stream);
+    case 8: return launch_rows<8>(p, wgs, stream);
+    case 9: return launch_rows<9>(p, wgs, stream);
+    case 10: return launch_rows<10>(p, wgs, stream);
+    case 11: return launch_rows<11>(p, wgs, stream);
+    default: return launch_rows<12>(p, wgs, stream);
+  }
+}
+
 int launch_q4k_matvec(const Q4kParams& p, hipStream_t stream) {
   const uint32_t kp = (p.K / 64 + 63) / 64;
-  if (kp == 1) return launch_kp<1>(p, stream);
+  if (kp == 1) return launch_rows_any(p, stream);
   if (kp == 2) return launch_kp<2>(p, stream);
   if (kp == 3) return launch_kp<3>(p, stream);
   if (kp == 4) return launch_kp<4>(p, stream);
