@@ -20,14 +20,14 @@
 // dequantisation kernel below reproduces the shader's f32 weights bit for
 // bit.
 //
-// K <= 4096 (one wave per row): wave w of the W waves of the grid owns rows
-// w, w + W, ..., at most 12 of them, with two rows in flight: row j + 2 is
-// requested as soon as row j is reduced, and the first two before x is
-// staged.  Eight waves per CU.  Measured against the same kernel with more
-// rows in flight (three to all twelve, or four waves per CU): two rows and
-// eight waves is the fastest for every projection shape; with more requests
-// in flight the rows come back in an order that leaves waves waiting on
-// their first row.
+// K <= 4096 (one wave per row): wave w owns the contiguous rows w*R ..
+// w*R + R-1 (R <= 12), with two rows in flight: row j + 2 is requested as
+// soon as row j is reduced, and the first two before x is staged.  Eight
+// waves per CU.  Measured per projection shape against the alternatives:
+// three to twelve rows in flight, four, twelve or sixteen waves per CU,
+// rows dealt round-robin over the waves, and nontemporal weight loads were
+// all slower (the last by up to 15% on the FFN's linear_in: the three loads
+// of a row share cache lines, which plain loads let the CU's cache serve).
 // K > 4096: KP waves share a row and combine through LDS; rows are dealt
 // round-robin to the row groups of the grid, two steps of U rows in flight.
 //
@@ -45,9 +45,6 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-}
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
@@ -123,8 +120,8 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
     for (int u = 0; u < U; ++u) {
       const size_t off = (size_t)min(base + grp * U + u, p.N - 1) * row_bytes;
       r.hd[u] = ld16(whead + off);
-      r.qa[u] = ld16_stream(wslot + off);
-      r.qb[u] = ld16_stream(wslot + off + 16);
+      r.qa[u] = ld16(wslot + off);
+      r.qb[u] = ld16(wslot + off + 16);
     }
   };
   // The first step's weights are requested before x, so both latencies overlap.
@@ -196,15 +193,13 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
   }
 }
 
-// K <= 4096: wave w owns rows w + j*W (j < R), two of them in flight.
+// K <= 4096: wave w owns rows w*R .. w*R + R-1, two of them in flight.
 constexpr int kRowsInFlight = 2;
 
 template <int R>
 __global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p) {
   const int lane = threadIdx.x & 63;
-  const uint32_t wpb = blockDim.x >> 6;
-  const uint32_t W = gridDim.x * wpb;
-  const uint32_t w = blockIdx.x * wpb + (threadIdx.x >> 6);
+  const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const uint32_t nb = p.K / kQ4kBlockWeights;
   const uint32_t s = lane;  // this lane's slot
   const bool has = s < 4u * nb;
@@ -234,10 +229,10 @@ __global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p)
   u32x4 hd[R], qa[R], qb[R];
   auto load = [&](int j) {
     // Rows past the end re-read row N-1 and are not stored.
-    const size_t off = (size_t)min(w + j * W, p.N - 1) * row_bytes;
+    const size_t off = (size_t)min(w * R + j, p.N - 1) * row_bytes;
     hd[j] = ld16(whead + off);
-    qa[j] = ld16_stream(wslot + off);
-    qb[j] = ld16_stream(wslot + off + 16);
+    qa[j] = ld16(wslot + off);
+    qb[j] = ld16(wslot + off + 16);
   };
   constexpr int D = kRowsInFlight < R ? kRowsInFlight : R;
 #pragma unroll
@@ -278,7 +273,7 @@ __global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p)
   if (lane == 0) {
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-      const uint32_t row = w + j * W;
+      const uint32_t row = w * R + j;
       if (row < p.N) {
         float v = acc[j];
         if (p.res) v += p.res[(size_t)b * p.N + row];
