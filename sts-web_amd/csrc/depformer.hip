@@ -37,9 +37,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
-__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-}
 
 // The 48 weight bytes lane (r, g) needs of one super-block row: header and
 // the 32 quant bytes of slot g.
@@ -77,8 +74,8 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
       const uint32_t n = min(t * 16 + r + (hv ? p.swiglu_f : 0u), p.N - 1);
       const uint8_t* blk = W + n * row_bytes + (size_t)kb * kQ4kBlockBytes;
       wt[hv].hd = ld16(blk);
-      wt[hv].qa = ld16_stream(blk + 16 + 32 * g);
-      wt[hv].qb = ld16_stream(blk + 32 + 32 * g);
+      wt[hv].qa = ld16(blk + 16 + 32 * g);
+      wt[hv].qb = ld16(blk + 32 + 32 * g);
     }
   };
   // The first tile's weights are requested before x, so both latencies overlap.
