@@ -351,10 +351,11 @@ int launch_rows(const Q4kParams& p, uint32_t wgs, hipStream_t stream) {
 }
 
 // K <= 4096: eight waves per CU, or as many more as keep each wave at 12
-// rows or fewer; R = rows per wave.
+// rows or fewer, and no more waves than rows; R = rows per wave.
 int launch_rows_any(const Q4kParams& p, hipStream_t stream) {
   const uint32_t cus = (uint32_t)device_cu_count();
-  const uint32_t wgs = (std::max(8u * cus, (p.N + 11) / 12) + 3) / 4;
+  const uint32_t waves = std::min(std::max(8u * cus, (p.N + 11) / 12), p.N);
+  const uint32_t wgs = (waves + 3) / 4;
   const uint32_t r = (p.N + 4 * wgs - 1) / (4 * wgs);
   switch (r) {
     case 1: return launch_rows<1>(p, wgs, stream);
