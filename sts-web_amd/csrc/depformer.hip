@@ -510,15 +510,29 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 }  // namespace
 
 int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
-  if (p.K > 16 * kQ4kBlockWeights && p.K % kQ4kBlockWeights == 0 && p.K <= 64 * kQ4kBlockWeights) {
+  // Every check runs before anything is allocated or launched.
+  if (p.K % kQ4kBlockWeights != 0 || p.K == 0 || p.K > 64 * kQ4kBlockWeights)
+    return fail(STS_ERR_INVALID, "GEMM K = %u must be a multiple of 256 in 256..16384", p.K);
+  if (p.M == 0 || p.N == 0 || p.Z == 0 || p.Z > (uint32_t)kGemmMaxZ)
+    return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u Z=%u", p.M, p.N, p.Z);
+  if ((p.M + 15) / 16 > 65535u) return fail(STS_ERR_INVALID, "M = %u too large", p.M);
+  if (p.swiglu_f && (p.swiglu_f * 2 != p.N))
+    return fail(STS_ERR_INVALID, "SwiGLU GEMM needs N = 2F (N=%u F=%u)", p.N, p.swiglu_f);
+  if (p.ldx % 4 != 0 || p.x_zstride % 4 != 0 || (reinterpret_cast<uintptr_t>(p.x) & 15))
+    return fail(STS_ERR_INVALID, "GEMM x rows must be 16-byte aligned");
+  for (uint32_t z = 0; z < p.Z; ++z)
+    if (!p.w[z] || (reinterpret_cast<uintptr_t>(p.w[z]) & 15))
+      return fail(STS_ERR_INVALID, "GEMM weights %u null or not 16-byte aligned", z);
+  if (p.K > 16 * kQ4kBlockWeights) {
     // Split K: slices of up to 16 super-blocks into a workspace, then the sum.
     if (p.Z != 1 || p.swiglu_f || p.norm_alpha)
       return fail(STS_ERR_INVALID, "GEMM with K = %u > 4096 takes no SwiGLU, RMSNorm or Z > 1",
                   p.K);
-    if (p.M == 0 || p.N == 0) return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u", p.M, p.N);
     const uint32_t KB = p.K / kQ4kBlockWeights;
     const uint32_t nsl = (KB + 15) / 16;
     const size_t mn = (size_t)p.M * p.N;
+    const uint64_t blocks = (mn + 255) / 256;
+    if (blocks > 0x7FFFFFFFull) return fail(STS_ERR_INVALID, "GEMM M x N = %zu too large", mn);
     Workspace* ws = nullptr;
     if (int rc = get_workspace(stream, nsl * mn, 0, &ws)) return rc;
     for (uint32_t sl = 0; sl < nsl; ++sl) {
@@ -533,23 +547,11 @@ int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
       q.ldy = p.N;
       if (int rc = launch_q4k_gemm(q, stream)) return rc;
     }
-    const uint64_t blocks = (mn + 255) / 256;
     hipLaunchKernelGGL(splitk_sum_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
                        ws->part, nsl, p.M, p.N, p.res, p.ldr, p.y, p.ldy);
     STS_HIP(hipGetLastError());
     return STS_OK;
   }
-  if (p.K % kQ4kBlockWeights != 0 || p.K == 0 || p.K > 16 * kQ4kBlockWeights)
-    return fail(STS_ERR_INVALID, "GEMM K = %u must be a multiple of 256 in 256..16384", p.K);
-  if (p.M == 0 || p.N == 0 || p.Z == 0 || p.Z > (uint32_t)kGemmMaxZ)
-    return fail(STS_ERR_INVALID, "GEMM shape M=%u N=%u Z=%u", p.M, p.N, p.Z);
-  if (p.swiglu_f && (p.swiglu_f * 2 != p.N))
-    return fail(STS_ERR_INVALID, "SwiGLU GEMM needs N = 2F (N=%u F=%u)", p.N, p.swiglu_f);
-  if (p.ldx % 4 != 0 || p.x_zstride % 4 != 0 || (reinterpret_cast<uintptr_t>(p.x) & 15))
-    return fail(STS_ERR_INVALID, "GEMM x rows must be 16-byte aligned");
-  for (uint32_t z = 0; z < p.Z; ++z)
-    if (!p.w[z] || (reinterpret_cast<uintptr_t>(p.w[z]) & 15))
-      return fail(STS_ERR_INVALID, "GEMM weights %u null or not 16-byte aligned", z);
   const uint32_t KB = p.K / kQ4kBlockWeights;
   const uint32_t mtiles = (p.M + 15) / 16;
   const uint32_t nout = p.swiglu_f ? p.swiglu_f : p.N;
@@ -558,7 +560,6 @@ int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
   // reads its 16 x rows once.
   const uint32_t cus = (uint32_t)device_cu_count();
   const uint32_t gx = std::max(1u, std::min(ntiles, 4 * cus / std::max(1u, mtiles * p.Z)));
-  if (mtiles > 65535u) return fail(STS_ERR_INVALID, "M = %u too large", p.M);
   const dim3 grid(gx, mtiles, p.Z), block(64 * KB);
   if (KB <= 4) {
     if (p.swiglu_f)

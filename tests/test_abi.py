@@ -294,6 +294,14 @@ def test_depformer_chain_argument_errors():
                                               64, 11264, 4096, 0, None))
     assert "multiple of 256" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 16640, None, 0.0, None, 0, FAKE,
                                                       4096, 64, 16640, 4096, 0, None))
+    # The summed-slice route checks the shape and alignment before it takes
+    # any workspace.
+    assert "too large" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 11264, None, 0.0, None, 0, FAKE, 4096,
+                                                16 * 65536 + 1, 11264, 4096, 0, None))
+    assert "aligned" in _err(lib.sts_q4k_gemm(FAKE, FAKE + 4, 11264, None, 0.0, None, 0, FAKE, 4096,
+                                              64, 11264, 4096, 0, None))
+    assert "aligned" in _err(lib.sts_q4k_gemm(FAKE + 4, FAKE, 11264, None, 0.0, None, 0, FAKE, 4096,
+                                              64, 11264, 4096, 0, None))
     assert "strides" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 512, None, 0.0, None, 0, FAKE, 3072, 64,
                                               1024, 3072, 0, None))
     assert "norm_eps" in _err(lib.sts_q4k_gemm(FAKE, FAKE, 1024, FAKE, -1.0, None, 0, FAKE, 3072,
