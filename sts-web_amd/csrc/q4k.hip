@@ -20,16 +20,18 @@
 // dequantisation kernel below reproduces the shader's f32 weights bit for
 // bit.
 //
-// K <= 4096 (one wave per row): wave w owns the contiguous rows w*R ..
-// w*R + R-1 (R <= 12), with two rows in flight: row j + 2 is requested as
-// soon as row j is reduced, and the first two before x is staged.  Eight
-// waves per CU.  Measured per projection shape against the alternatives:
-// three to twelve rows in flight, four, twelve or sixteen waves per CU,
-// rows dealt round-robin over the waves, and nontemporal weight loads were
-// all slower (the last by up to 15% on the FFN's linear_in: the three loads
-// of a row share cache lines, which plain loads let the CU's cache serve).
-// K > 4096: KP waves share a row and combine through LDS; rows are dealt
-// round-robin to the row groups of the grid, two steps of U rows in flight.
+// Rows are dealt to groups of KP waves (KP = 1 up to K = 4096): group g owns
+// the contiguous rows g*R .. g*R + R-1 (R <= 12), with two rows in flight:
+// row j + 2 is requested as soon as row j is reduced, and the first two
+// before x is staged.  The KP waves of a group keep their partial sums and
+// combine through LDS once, at the end.  K <= 4096: eight waves per CU in
+// workgroups of four; K > 4096: one workgroup of 12 waves per CU, so that x
+// is staged once per CU.  Measured per projection shape against the
+// alternatives: three to twelve rows in flight, four, twelve or sixteen
+// waves per CU at K <= 4096, rows dealt round-robin over the waves, and
+// nontemporal weight loads were all slower (the last by up to 15% on the
+// FFN's linear_in: the three loads of a row share cache lines, which plain
+// loads let the CU's cache serve).
 //
 // HBM-bound: 0.5625 bytes and 2 flops per weight (x and y are negligible).
 #include <algorithm>
@@ -88,15 +90,23 @@ __device__ __forceinline__ float wave_sum(float x) {
   return sum_xor32(sum_xor16(x));
 }
 
-// K > 4096: KP waves share a row (slots 64*kp + lane) and combine through
-// LDS, G row groups per workgroup, U rows per group per step, two steps in
-// flight.  grid.y = batch.
-template <int KP, int G, int U>
-__global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams p) {
+// Group g of the grid owns the contiguous rows g*R .. g*R + R-1; its KP
+// waves cover slots 64*kp + lane of each of them (KP = 1 up to K = 4096),
+// with two rows in flight, and keep their partial sums until the end, where
+// the KP waves of a group combine through LDS once.  G groups per
+// workgroup.
+constexpr int kRowsInFlight = 2;
+
+template <int R, int KP, int G>
+__global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kParams p) {
+  constexpr int NT = 64 * KP * G;     // threads
+  constexpr int XL = (1024 * KP + NT - 1) / NT;  // float4 of x per thread, K <= 4096 KP
+  static_assert(XL >= 1 && XL * NT >= 1024 * KP, "x staging shape");
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int kp = wv % KP;
   const int grp = wv / KP;
+  const uint32_t row0 = (blockIdx.x * G + grp) * R;  // this group's first row
   const uint32_t nb = p.K / kQ4kBlockWeights;
   const uint32_t s = 64u * kp + lane;  // this lane's slot
   const bool has = s < 4u * nb;
@@ -104,132 +114,37 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_kernel(const Q4kParams
   // its x values and their sums are zero.
   const uint32_t blk = has ? s >> 2 : 0u, it = has ? s & 3u : 0u;
   const uint32_t b = blockIdx.y;
-
-  __shared__ float red[G][U][KP];
-  const size_t row_bytes = (size_t)nb * kQ4kBlockBytes;
-  const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
-  const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
-  const uint32_t stride = gridDim.x * (G * U);
-
-  struct Rows {
-    u32x4 hd[U], qa[U], qb[U];
-  };
-  // Rows past the end re-read row N-1 and are not stored.
-  auto load = [&](Rows& r, uint32_t base) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const size_t off = (size_t)min(base + grp * U + u, p.N - 1) * row_bytes;
-      r.hd[u] = ld16(whead + off);
-      r.qa[u] = ld16(wslot + off);
-      r.qb[u] = ld16(wslot + off + 16);
-    }
-  };
-  // The first step's weights are requested before x, so both latencies overlap.
-  Rows ra, rb;
-  uint32_t base = blockIdx.x * (G * U);
-  load(ra, base);
-
-  // This lane's 64 x values, kept in registers for the whole launch.  The
-  // workgroup reads x once with coalesced loads into LDS, slot c at row c of
-  // pitch 68 floats (the 16 lanes of a read phase then hit distinct banks),
-  // and each lane copies its slot.
-  extern __shared__ __align__(16) float xs[];  // [K/64][68]
-  {
-    const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
-    const uint32_t n4 = p.K / 4;
-    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x)
-      *reinterpret_cast<float4*>(&xs[(i >> 4) * 68 + 4 * (i & 15)]) = xb[i];
-    __syncthreads();
-  }
-  float xv[64];
-  const uint32_t xs0 = has ? s * 68 : 0u;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float4 t = *reinterpret_cast<const float4*>(&xs[xs0 + 4 * j]);
-    xv[4 * j] = has ? t.x : 0.f;
-    xv[4 * j + 1] = has ? t.y : 0.f;
-    xv[4 * j + 2] = has ? t.z : 0.f;
-    xv[4 * j + 3] = has ? t.w : 0.f;
-  }
-  float sxl = 0.f, sxh = 0.f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    sxl += xv[j];
-    sxh += xv[32 + j];
-  }
-
-  auto finish = [&](const Rows& r, uint32_t base) {
-    float acc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      acc[u] = wave_sum(slot_dot(r.hd[u], r.qa[u], r.qb[u], 2 * it, xv, sxl, sxh));
-    const uint32_t r0 = base + grp * U;
-    if (lane == 0) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) red[grp][u][kp] = acc[u];
-    }
-    __syncthreads();
-    if (kp == 0 && lane < U) {
-      const uint32_t row = r0 + lane;
-      if (row < p.N) {
-        float v = red[grp][lane][0];
-#pragma unroll
-        for (int k = 1; k < KP; ++k) v += red[grp][lane][k];
-        if (p.res) v += p.res[(size_t)b * p.N + row];
-        p.y[(size_t)b * p.N + row] = v;
-      }
-    }
-    __syncthreads();
-  };
-
-  // Two steps in flight: while one set of rows is reduced, the next loads.
-  // The loop bound is uniform over the workgroup (it depends on blockIdx
-  // only), as the barriers of the KP > 1 combine require.
-  for (; base < p.N; base += 2 * stride) {
-    load(rb, base + stride);
-    finish(ra, base);
-    load(ra, base + 2 * stride);
-    if (base + stride < p.N) finish(rb, base + stride);
-  }
-}
-
-// K <= 4096: wave w owns rows w*R .. w*R + R-1, two of them in flight.
-constexpr int kRowsInFlight = 2;
-
-template <int R>
-__global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const uint32_t nb = p.K / kQ4kBlockWeights;
-  const uint32_t s = lane;  // this lane's slot
-  const bool has = s < 4u * nb;
-  // A lane without a slot reads slot 0 (valid memory) and contributes zero:
-  // its x values and their sums are zero.
-  const uint32_t blk = has ? s >> 2 : 0u, it = has ? s & 3u : 0u;
-  const uint32_t b = blockIdx.y;
   const size_t row_bytes = (size_t)nb * kQ4kBlockBytes;
   const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
   const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
 
-  // x (at most 4096 floats, 1024 float4) is requested first, then the first
-  // rows, so that waiting for x does not wait for the weights.  The
-  // workgroup stages x in LDS, slot c at row c of pitch 68 floats (the 16
-  // lanes of a read phase then hit distinct banks), and each lane copies its
-  // slot into registers.
+  // x is requested first, then the first rows, so that waiting for x does
+  // not wait for the weights.  The workgroup stages x in LDS, slot c at row c
+  // of pitch 68 floats (the 16 lanes of a read phase then hit distinct
+  // banks), and each lane copies its slot into registers.
   extern __shared__ __align__(16) float xs[];  // [K/64][68]
   const float4* xb = reinterpret_cast<const float4*>(p.x + (size_t)b * p.K);
   const uint32_t n4 = p.K / 4;
-  const uint32_t i0 = threadIdx.x, i1 = i0 + blockDim.x, i2 = i1 + blockDim.x,
-                 i3 = i2 + blockDim.x;
-  const float4 x0 = xb[i0 < n4 ? i0 : 0u], x1 = xb[i1 < n4 ? i1 : 0u],
-               x2 = xb[i2 < n4 ? i2 : 0u], x3 = xb[i3 < n4 ? i3 : 0u];
+  // A vector value, not an array: an array would be kept in scratch memory
+  // across the scheduling barrier below.
+  typedef float xvec __attribute__((ext_vector_type(4 * XL)));
+  xvec xr;
+#pragma unroll
+  for (int k = 0; k < XL; ++k) {
+    const uint32_t i = threadIdx.x + k * NT;
+    const float4 t = xb[i < n4 ? i : 0u];
+    xr[4 * k] = t.x;
+    xr[4 * k + 1] = t.y;
+    xr[4 * k + 2] = t.z;
+    xr[4 * k + 3] = t.w;
+  }
   // Keeps the x loads ahead of the weight loads in the issue order.
   __builtin_amdgcn_sched_barrier(0);
 
   u32x4 hd[R], qa[R], qb[R];
   auto load = [&](int j) {
     // Rows past the end re-read row N-1 and are not stored.
-    const size_t off = (size_t)min(w * R + j, p.N - 1) * row_bytes;
+    const size_t off = (size_t)min(row0 + j, p.N - 1) * row_bytes;
     hd[j] = ld16(whead + off);
     qa[j] = ld16(wslot + off);
     qb[j] = ld16(wslot + off + 16);
@@ -239,13 +154,13 @@ __global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p)
   for (int j = 0; j < D; ++j) load(j);
   __builtin_amdgcn_sched_barrier(0);
 
-  auto stage = [&](uint32_t i, const float4& v) {
-    if (i < n4) *reinterpret_cast<float4*>(&xs[(i >> 4) * 68 + 4 * (i & 15)]) = v;
-  };
-  stage(i0, x0);
-  stage(i1, x1);
-  stage(i2, x2);
-  stage(i3, x3);
+#pragma unroll
+  for (int k = 0; k < XL; ++k) {
+    const uint32_t i = threadIdx.x + k * NT;
+    if (i < n4)
+      *reinterpret_cast<float4*>(&xs[(i >> 4) * 68 + 4 * (i & 15)]) =
+          make_float4(xr[4 * k], xr[4 * k + 1], xr[4 * k + 2], xr[4 * k + 3]);
+  }
   __syncthreads();
   float xv[64];
   const uint32_t xs0 = has ? s * 68 : 0u;
@@ -270,15 +185,34 @@ __global__ __launch_bounds__(256) void q4k_matvec_rows_kernel(const Q4kParams p)
     acc[j] = wave_sum(slot_dot(hd[j], qa[j], qb[j], 2 * it, xv, sxl, sxh));
     if (j + D < R) load(j + D);
   }
-  if (lane == 0) {
+  auto store = [&](int j, float v) {
+    const uint32_t row = row0 + j;
+    if (row < p.N) {
+      if (p.res) v += p.res[(size_t)b * p.N + row];
+      p.y[(size_t)b * p.N + row] = v;
+    }
+  };
+  if constexpr (KP == 1) {
+    if (lane == 0) {
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-      const uint32_t row = w * R + j;
-      if (row < p.N) {
-        float v = acc[j];
-        if (p.res) v += p.res[(size_t)b * p.N + row];
-        p.y[(size_t)b * p.N + row] = v;
-      }
+      for (int j = 0; j < R; ++j) store(j, acc[j]);
+    }
+  } else {
+    // x is in registers by now: its LDS rows hold the partial sums, in the
+    // order of the slots (wave 0 first), so the sum runs as the KP = 1
+    // kernel would add the waves' shares.
+    __syncthreads();
+    float* red = xs;  // [G][R][KP]
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < R; ++j) red[(grp * R + j) * KP + kp] = acc[j];
+    }
+    __syncthreads();
+    if (kp == 0 && lane < R) {
+      float v = red[(grp * R + lane) * KP];
+#pragma unroll
+      for (int k = 1; k < KP; ++k) v += red[(grp * R + lane) * KP + k];
+      store(lane, v);
     }
   }
 }
@@ -321,64 +255,52 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
   }
 }
 
-template <int KP>
-int launch_kp(const Q4kParams& p, hipStream_t stream) {
-  static_assert(KP > 1, "K <= 4096 runs q4k_matvec_rows_kernel");
-  constexpr int G = KP == 2 ? 2 : 1;
-  constexpr int U = 2;
-  // Eight waves per CU walking the rows; each workgroup reads x once into
-  // LDS.  Measured for FFN linear_out [4096, 11264]: 12.7 us against 14.1
-  // with four.
-  const uint32_t waves_per_cu = 8;
-  const uint32_t cus = (uint32_t)device_cu_count();
-  const uint32_t steps = (p.N + G * U - 1) / (G * U);
-  const uint32_t wgs = std::max(1u, std::min(steps, cus * waves_per_cu / (KP * G)));
-  const size_t lds = (size_t)(p.K / 64) * 68 * sizeof(float);
-  hipLaunchKernelGGL((q4k_matvec_kernel<KP, G, U>), dim3(wgs, p.B), dim3(64 * KP * G), lds,
+template <int R, int KP, int G>
+int launch_rows(const Q4kParams& p, uint32_t wgs, hipStream_t stream) {
+  const size_t lds = std::max((size_t)(p.K / 64) * 68, (size_t)G * R * KP) * sizeof(float);
+  hipLaunchKernelGGL((q4k_matvec_rows_kernel<R, KP, G>), dim3(wgs, p.B), dim3(64 * KP * G), lds,
                      stream, p);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }
 
-}  // namespace
-
-template <int R>
-int launch_rows(const Q4kParams& p, uint32_t wgs, hipStream_t stream) {
-  const size_t lds = (size_t)(p.K / 64) * 68 * sizeof(float);
-  hipLaunchKernelGGL((q4k_matvec_rows_kernel<R>), dim3(wgs, p.B), dim3(256), lds, stream, p);
-  STS_HIP(hipGetLastError());
-  return STS_OK;
-}
-
-// K <= 4096: eight waves per CU, or as many more as keep each wave at 12
-// rows or fewer, and no more waves than rows; R = rows per wave.
-int launch_rows_any(const Q4kParams& p, hipStream_t stream) {
+// K <= 4096: eight waves per CU in workgroups of four.  K > 4096: one
+// workgroup of G groups (12 waves) per CU, so that x, up to 64 KB, is staged
+// once per CU (for the FFN's linear_out [4096, 11264]: 7.3 us, against 8.3
+// with two groups per workgroup and 9.4-11.0 with one).  In both cases as
+// many more groups as keep each at 12 rows or fewer, and no more groups than
+// rows; R = rows per group.
+template <int KP, int G>
+int launch_rows_kp(const Q4kParams& p, hipStream_t stream) {
   const uint32_t cus = (uint32_t)device_cu_count();
-  const uint32_t waves = std::min(std::max(8u * cus, (p.N + 11) / 12), p.N);
-  const uint32_t wgs = (waves + 3) / 4;
-  const uint32_t r = (p.N + 4 * wgs - 1) / (4 * wgs);
+  const uint32_t min_groups = KP == 1 ? 8u * cus : G * cus;
+  const uint32_t groups = std::min(std::max(min_groups, (p.N + 11) / 12), p.N);
+  const uint32_t wgs = (groups + G - 1) / G;
+  const uint32_t r = (p.N + G * wgs - 1) / (G * wgs);
   switch (r) {
-    case 1: return launch_rows<1>(p, wgs, stream);
-    case 2: return launch_rows<2>(p, wgs, stream);
-    case 3: return launch_rows<3>(p, wgs, stream);
-    case 4: return launch_rows<4>(p, wgs, stream);
-    case 5: return launch_rows<5>(p, wgs, stream);
-    case 6: return launch_rows<6>(p, wgs, stream);
-    case 7: return launch_rows<7>(p, wgs, stream);
-    case 8: return launch_rows<8>(p, wgs, stream);
-    case 9: return launch_rows<9>(p, wgs, stream);
-    case 10: return launch_rows<10>(p, wgs, stream);
-    case 11: return launch_rows<11>(p, wgs, stream);
-    default: return launch_rows<12>(p, wgs, stream);
+    case 1: return launch_rows<1, KP, G>(p, wgs, stream);
+    case 2: return launch_rows<2, KP, G>(p, wgs, stream);
+    case 3: return launch_rows<3, KP, G>(p, wgs, stream);
+    case 4: return launch_rows<4, KP, G>(p, wgs, stream);
+    case 5: return launch_rows<5, KP, G>(p, wgs, stream);
+    case 6: return launch_rows<6, KP, G>(p, wgs, stream);
+    case 7: return launch_rows<7, KP, G>(p, wgs, stream);
+    case 8: return launch_rows<8, KP, G>(p, wgs, stream);
+    case 9: return launch_rows<9, KP, G>(p, wgs, stream);
+    case 10: return launch_rows<10, KP, G>(p, wgs, stream);
+    case 11: return launch_rows<11, KP, G>(p, wgs, stream);
+    default: return launch_rows<12, KP, G>(p, wgs, stream);
   }
 }
 
+}  // namespace
+
 int launch_q4k_matvec(const Q4kParams& p, hipStream_t stream) {
   const uint32_t kp = (p.K / 64 + 63) / 64;
-  if (kp == 1) return launch_rows_any(p, stream);
-  if (kp == 2) return launch_kp<2>(p, stream);
-  if (kp == 3) return launch_kp<3>(p, stream);
-  if (kp == 4) return launch_kp<4>(p, stream);
+  if (kp == 1) return launch_rows_kp<1, 4>(p, stream);
+  if (kp == 2) return launch_rows_kp<2, 6>(p, stream);
+  if (kp == 3) return launch_rows_kp<3, 4>(p, stream);
+  if (kp == 4) return launch_rows_kp<4, 3>(p, stream);
   return fail(STS_ERR_INVALID, "K = %u too large (at most 16384)", p.K);
 }
 

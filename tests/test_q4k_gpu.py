@@ -73,7 +73,8 @@ def test_dequant_of_quantized_weights(gpu):
 @pytest.mark.parametrize("N,K,B", [(12288, 4096, 1), (4096, 4096, 1), (22528, 4096, 1),
                                    (4096, 11264, 1), (3072, 1024, 1), (1024, 2816, 1),
                                    (1001, 4096, 3), (5, 8192, 2), (17, 16384, 1), (1, 256, 1),
-                                   (16000, 256, 2), (30000, 512, 1)])
+                                   (16000, 256, 2), (30000, 512, 1), (3000, 6144, 2),
+                                   (700, 12288, 1), (9000, 11264, 1)])
 def test_matvec_against_oracle(gpu, N, K, B):
     print(f"q4k matvec N={N} K={K} B={B}", flush=True)
     blocks = oracle.q4k_random_blocks(N + K + B, N, K)
