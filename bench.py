@@ -275,7 +275,8 @@ def bench_q4k(torch, sts, stream, steps, warmup):
     frame 24 layers x (in_proj [12288, 4096] + out_proj [4096, 4096] with the
     residual), each layer with its own weights (905 MB, beyond the MALL),
     launched eagerly and replayed from a HIP graph; plus single-launch rates of
-    the FFN shapes linear_in [22528, 4096] and linear_out [4096, 11264]."""
+    the FFN shapes linear_in [22528, 4096] and linear_out [4096, 11264]
+    (four weight sets each, 32 launches per graph replay)."""
     g = torch.Generator(device="cuda").manual_seed(6)
     K = 4096
     layers = [(sts.Q4KTensor(q4k_random(torch, g, 3 * K, K), (3 * K, K)),
@@ -316,14 +317,23 @@ def bench_q4k(torch, sts, stream, steps, warmup):
         yo = torch.empty((1, 1, n), device="cuda")
         for w in ws:
             sts.q4k_matmul(xi, w, out=yo, stream=stream)
-        with Timer(torch, stream) as t:
-            for _ in range(steps):
+        # Replayed from a graph of 32 launches: an eager Python-side launch,
+        # or a graph of only a few, costs more than these kernels take.
+        reps = 8
+        gl = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gl, stream=stream):
+            for _ in range(reps):
                 for w in ws:
                     sts.q4k_matmul(xi, w, out=yo, stream=stream)
-        us_l = t.ms * 1e3 / (steps * len(ws))
+        for _ in range(warmup):
+            gl.replay()
+        with Timer(torch, stream) as t:
+            for _ in range(steps):
+                gl.replay()
+        us_l = t.ms * 1e3 / (steps * reps * len(ws))
         res[name + "_us_per_launch"] = us_l
         res[name + "_gbs"] = n * k // 256 * 144 / (us_l * 1e-6) / 1e9
-        del ws
+        del gl, ws
     return res
 
 
