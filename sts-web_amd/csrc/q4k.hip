@@ -52,6 +52,8 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
 }
 
 // d1*sum(q_lo*x_lo) - m1*sum(x_lo) + d2*sum(q_hi*x_hi) - m2*sum(x_hi) for one slot.
+// xv[32..63] hold x_hi / 16 (the high nibbles are taken in place, as 16 q_hi);
+// sxl and sxh are the sums of the unscaled x_lo and x_hi.
 __device__ __forceinline__ float slot_dot(u32x4 hd, u32x4 qa, u32x4 qb, uint32_t jl,
                                           const float (&xv)[64], float sxl, float sxh) {
   const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
@@ -65,7 +67,7 @@ __device__ __forceinline__ float slot_dot(u32x4 hd, u32x4 qa, u32x4 qb, uint32_t
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
     uint32_t lo = words[w] & 0x0F0F0F0Fu;
-    uint32_t hi = (words[w] >> 4) & 0x0F0F0F0Fu;
+    uint32_t hi = words[w] & 0xF0F0F0F0u;  // 16 q: its x values are scaled by 1/16
     // Opaque to the optimiser, so that each byte below becomes one
     // v_cvt_f32_ubyte{0..3} instead of a bit-field extract plus a convert.
     asm("" : "+v"(lo), "+v"(hi));
@@ -178,6 +180,10 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kP
     sxl += xv[j];
     sxh += xv[32 + j];
   }
+  // The high-nibble products take the nibble in place (16 q, one mask, no
+  // shift) times x / 16: both scalings are exact, so the products are q x.
+#pragma unroll
+  for (int j = 0; j < 32; ++j) xv[32 + j] *= 0.0625f;
 
   float acc[R];
 #pragma unroll
