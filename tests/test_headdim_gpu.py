@@ -103,3 +103,55 @@ def test_kv_handle_decode_step_and_prefill(gpu, D):
     assert np.abs(got - ref).max() < TOL
     seq = oracle.prefill_seq_wgsl(q, kc, vc, 230, 160, scale_for(D))
     assert np.abs(got - seq).max() < TOL
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,M", [(8, 2, 96, 150), (6, 3, 32, 100)])
+def test_gqa_at_padded_head_dims(gpu, Hq, Hkv, D, M):
+    """Grouped-query attention (model.rs:766-783) at a head dim that runs the
+    padded decode kernel: chunked prefill with RoPE (every precision asks for
+    the same f32 per-query decodes here), the fused decode step and attend,
+    bit for bit against a handle holding the expanded K/V heads and within
+    1e-4 of the f64 closed form over the expanded caches."""
+    print(f"gqa head_dim Hq={Hq} Hkv={Hkv} D={D} M={M}", flush=True)
+    rep = Hq // Hkv
+    rope = sts_attn.RoPE(D, 4096)
+    tabs = oracle.rope_tables(D, 4096)
+    g = sts_attn.KVCache(M, Hkv, D, n_heads=Hq)
+    e = sts_attn.KVCache(M, Hq, D)
+    o = oracle.KvCounters(M)
+    kref = np.zeros((1, Hkv, M, D), np.float32)
+    vref = np.zeros((1, Hkv, M, D), np.float32)
+    for it, S in enumerate((90, 1, 45, 3, 1)):
+        q = oracle.normal(400 + it, (1, S, Hq, D))
+        k = oracle.normal(410 + it, (1, S, Hkv, D))
+        v = oracle.normal(420 + it, (1, S, Hkv, D))
+        ke, ve = np.repeat(k, rep, axis=2), np.repeat(v, rep, axis=2)
+        if S == 1:
+            got = host(g.decode_step(dev(q[:, 0]), dev(k[:, 0]), dev(v[:, 0]), scale_for(D),
+                                     rope=rope))
+            want = host(e.decode_step(dev(q[:, 0]), dev(ke[:, 0]), dev(ve[:, 0]), scale_for(D),
+                                      rope=rope))
+        else:
+            got = host(g.prefill(dev(q[0]), dev(k[0]), dev(v[0]), scale_for(D),
+                                 sts_attn.PREC_BF16_MFMA, rope=rope))
+            want = host(e.prefill(dev(q[0]), dev(ke[0]), dev(ve[0]), scale_for(D),
+                                  sts_attn.PREC_BF16_MFMA, rope=rope))
+        np.testing.assert_array_equal(got, want)
+        qr = oracle.rope_apply(q, o.offset, tabs)[0]
+        kr = oracle.rope_apply(k, o.offset, tabs)
+        oracle.cache_write(kr, kref, o.offset % M, M)
+        oracle.cache_write(v, vref, o.offset % M, M)
+        o.advance(S)
+        kb, vb = g.read_buffers()
+        np.testing.assert_array_equal(host(kb), kref)
+        np.testing.assert_array_equal(host(vb), vref)
+        kx, vx = oracle.gqa_expand(kref[0], rep), oracle.gqa_expand(vref[0], rep)
+        ref = oracle.prefill_f64(qr, kx, vx, o.window_start(), o.len, scale_for(D))
+        assert np.abs(got.reshape(S, Hq, D) - ref).max() < TOL, it
+    qa = oracle.normal(499, (1, Hq, D))
+    got = host(g.attend(dev(qa), scale_for(D)))
+    np.testing.assert_array_equal(got, host(e.attend(dev(qa), scale_for(D))))
+    ref = oracle.attention_ring_f64(qa[0], oracle.gqa_expand(kref[0], rep),
+                                    oracle.gqa_expand(vref[0], rep), o.window_start(), o.len,
+                                    scale_for(D))
+    assert np.abs(got[0] - ref).max() < TOL
