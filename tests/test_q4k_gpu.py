@@ -153,3 +153,45 @@ def test_matmul_many_rows(gpu, N, K, B, Mrows, residual):
         ref = ref + r
         tol = tol + 1e-6 * np.abs(r)
     assert (np.abs(got.reshape(B * Mrows, N).astype(np.float64) - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("N,K,B", [(4096, 11264, 2), (300, 8192, 3), (77, 16384, 1)])
+def test_matvec_residual_split_rows(gpu, N, K, B):
+    """q4k_matmul_with_residual (gguf.rs:899-905) where several waves share a
+    row (K > 4096) and the batch has several rows: within the f32 bound of the
+    f64 product plus residual."""
+    print(f"q4k matvec+res N={N} K={K} B={B}", flush=True)
+    blocks = oracle.q4k_random_blocks(3 * N + K + B, N, K)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    x = oracle.normal(N + 17 * B, (B, 1, K))
+    res = oracle.normal(N + 19 * B, (B, 1, N))
+    got = host(sts_attn.q4k_matmul_with_residual(dev(x), w, dev(res)))[:, 0].astype(np.float64)
+    ref = oracle.q4k_matvec_f64(blocks, x[:, 0], N) + res[:, 0].astype(np.float64)
+    tol = 1e-5 * bound(blocks, x[:, 0], N) + 1e-6 * np.abs(res[:, 0])
+    assert (np.abs(got - ref) <= tol).all()
+
+
+def test_gemm_split_k_padded_strides(gpu):
+    """sts_q4k_gemm with k above 4096 (summed slices) and x, y and residual rows
+    wider than the products (ldx > k, ldy > n, ldr > n): the padding is neither
+    read into the sums nor written."""
+    N, K, M = 200, 8704, 7
+    ldx, ldy, ldr = K + 64, N + 40, N + 24
+    blocks = oracle.q4k_random_blocks(91, N, K)
+    w = sts_attn.Q4KTensor.from_q4k_bytes(blocks, (N, K))
+    xf = oracle.normal(92, (M, K))
+    rf = oracle.normal(93, (M, N))
+    xp = np.full((M, ldx), np.nan, np.float32)
+    xp[:, :K] = xf
+    rp = np.full((M, ldr), np.nan, np.float32)
+    rp[:, :N] = rf
+    x, r = dev(xp), dev(rp)
+    y = torch.full((M, ldy), -7.0, device="cuda")
+    lib = sts_attn.load()
+    assert lib.sts_q4k_gemm(w.raw.data_ptr(), x.data_ptr(), ldx, None, 0.0, r.data_ptr(), ldr,
+                            y.data_ptr(), ldy, M, K, N, 0, None) == 0
+    got = host(y)
+    assert (got[:, N:] == -7.0).all()
+    ref = oracle.q4k_matvec_f64(blocks, xf, N) + rf.astype(np.float64)
+    tol = 1e-5 * bound(blocks, xf, N) + 1e-6 * np.abs(rf)
+    assert (np.abs(got[:, :N].astype(np.float64) - ref) <= tol).all()
