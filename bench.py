@@ -1,14 +1,16 @@
 """Benchmark of the sts-web attention hot path on one MI355X.
 
-Headline: one temporal frame = 24 sequential layer
+Headline (the decode configuration, config 2): one temporal frame = 24 sequential layer
 decode steps, each a fused RoPE + append + attention (sts_kv_decode_step)
 over a 32-head x 128 f32 ring cache holding 3000 rows, with the write head at
 a seeded offset so reads wrap.  Every layer has its own 98 MB cache (2.36 GB,
 beyond the 256 MB MALL).  Inputs are resident in HBM before timing.
 
 Also reported (extra fields): decode without the append (sts_kv_attend),
-chunked prefill (config 3, f32, bf16-MFMA and split-bf16 f32), depformer frame (config 4),
-ragged multi-stream decode (config 5), the Q4_K projections around attention
+chunked prefill (config 3: 512 new rows after 256 cached, 32 x 128; f32,
+bf16-MFMA and split-bf16 f32), depformer step attention (config 4: 6 layers x 8
+steps, 64 streams, 16 x 64), ragged multi-stream decode (config 5: 64 streams,
+windows of 128-3000 rows), the Q4_K projections around attention
 (in_proj / out_proj per frame, FFN shapes), the whole depformer step chain for
 64 streams (depth_engine.rs:884-1491); and the CPU baseline -- the oracle's
 restatement of the reference shader, timed on this host's cores on a bounded

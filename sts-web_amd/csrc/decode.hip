@@ -290,8 +290,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   };
   // One batch of 16 rows in flight per wave (16 KB, 64 KB per CU): loads,
   // then the online-softmax update.  Deeper register pipelines (2-4 batches)
-  // lowered the HBM rate through the extra outstanding requests (config 2:
-  // 19.4 us per launch with one batch, 20.4-21.1 us with 2-4).
+  // lowered the HBM rate through the extra outstanding requests (32 heads x
+  // 128, 3000 rows: 19.4 us per launch with one batch, 20.4-21.1 us with 2-4).
   const uint32_t ustep = nsplit * WAVES;
   uint32_t u = split + nsplit * wave;
   float4 kk[RPG], vv[RPG];

@@ -1,6 +1,6 @@
 """Seeded input builders shared by the fixture generator and the GPU tests.
 
-All inputs follow the BASELINE configs' recipe: Q, K, V drawn N(0,1) from
+All inputs follow one recipe: Q, K, V drawn N(0,1) from
 the oracle's SplitMix64 / Box-Muller generator, RoPE (theta 1e4, interleaved)
 applied to Q and K at their logical positions, K/V rows written into a ring
 cache [B, H, M, D] whose window starts at slot `start` (so reads wrap).

@@ -96,7 +96,7 @@ def depformer_case(seed, wseed):
 
 
 CASES = {
-    # 1 layer, 32 x 128, L = 256, window at slot 0.
+    # The plumbing case: 1 layer, 32 x 128, L = 256, window at slot 0.
     "decode_config1": lambda: decode_case(101, 32, 128, 256, 256, 0),
     # Small wrapped windows (both head sizes), L = 1, and a window longer than 256 lanes.
     "decode_wrap_d64": lambda: decode_case(202, 4, 64, 9, 7, 5),

@@ -1,4 +1,6 @@
-"""Decode attention on the GPU against the oracle (2, 4, 5).
+"""Decode attention on the GPU against the oracle: the plumbing case (32 x 128,
+L = 256), the temporal decode (32 x 128, a wrapped 3000-row ring), the
+depformer steps (16 x 64, L = 1..8, 64 streams) and ragged multi-stream decode.
 
 Tolerance: f32 outputs within 1e-4 max-abs of the oracle (shader order and
 double closed form), the north star's f32 bar.  L = 1 and repeated runs are
@@ -39,7 +41,8 @@ def decode_fixture_inputs(f):
 
 
 def test_fused_attention_config1_golden(gpu):
-    """BASELINE config 1 through the drop-in fused_attention entry point."""
+    """The plumbing case (1 layer, 32 x 128, L = 256) through the drop-in
+    fused_attention entry point."""
     f = load_fixture("decode_config1")
     q, kc, vc = decode_fixture_inputs(f)
     H, M, D = kc.shape
@@ -109,7 +112,7 @@ def test_window_lengths_around_tile_edges(gpu, D, L):
 
 
 def test_config2_full_size_layers(gpu):
-    """BASELINE config 2 shape: 32 x 128, L = M = 3000, seeded write heads so the
+    """The temporal decode shape: 32 x 128, L = M = 3000, seeded write heads so the
     window wraps; three of the 24 layers checked against both oracles."""
     H, D, M = 32, 128, 3000
     rng = np.random.default_rng(2)
@@ -142,7 +145,7 @@ def test_repeat_runs_are_bit_identical(gpu):
 
 
 def test_config5_ragged_streams(gpu):
-    """64 streams x 32 x 128, per-stream L ~ U[128, 3000] and a
+    """Ragged multi-stream decode: 64 streams x 32 x 128, per-stream L ~ U[128, 3000] and a
     random ring start, plus edge streams (L = 0, 1, max_len; start = M - 1)."""
     B, H, D, M = 64, 32, 128, 3000
     rng = np.random.default_rng(5)
@@ -170,7 +173,7 @@ def test_config5_ragged_streams(gpu):
 
 
 def test_config4_depformer_frame(gpu):
-    """6 layers x 8 steps, 64 streams, 16 x 64, M = 9, no RoPE.
+    """The depformer step attention: 6 layers x 8 steps, 64 streams, 16 x 64, M = 9, no RoPE.
     Each step appends at slot `step` from a packed qkv buffer and attends slots
     0..step; outputs and the appended cache rows are checked every step."""
     B, H, D, M, layers, steps = 64, 16, 64, 9, 6, 8

@@ -1,5 +1,5 @@
-"""The timed headline path at its own shape: sts_kv_decode_step at BASELINE
-config 2 (32 heads x 128, a full 3000-row ring whose window wraps), the
+"""The timed headline path at its own shape: sts_kv_decode_step at the temporal
+decode shape (32 heads x 128, a full 3000-row ring whose window wraps), the
 multi-split 4-wave kernel with its fused RoPE + append.
 
 The decode branch of Q4Attention::forward_with_cache (model.rs:818-831):
@@ -40,7 +40,7 @@ def ropes(gpu):
 
 
 @pytest.mark.parametrize("B,H,D,use_rope,prefix", [
-    (1, 32, 128, True, 0),    # config 2: full ring, the append overwrites the oldest row
+    (1, 32, 128, True, 0),    # full ring: the append overwrites the oldest row
     (1, 32, 128, False, 0),
     (3, 32, 128, True, 0),
     (1, 32, 128, True, 1),    # 2999 rows before the step: the step fills the ring

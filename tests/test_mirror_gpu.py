@@ -6,8 +6,8 @@ values, written by every append made through the handle, and its bf16 prefill
 reads them instead: half the K/V bytes, the same stages, so the result must be
 bit-identical to the f32-input kernel's.  Checked here:
   - sts_prefill_attention_bf16kv over torch's bf16 rounding of the caches
-    equals sts_prefill_attention(PREC_BF16_MFMA) bit for bit (config 3 shape,
-    head_dim 64, ragged last tile, wrapped windows), and is within the bf16
+    equals sts_prefill_attention(PREC_BF16_MFMA) bit for bit (512 new rows after
+    256 cached, head_dim 64, ragged last tile, wrapped windows), and is within the bf16
     bar (2e-2) of the f64 oracle;
   - the mirror equals torch's bf16 rounding of the f32 caches, bit for bit,
     after chunk appends that wrap, fused decode steps with RoPE, prefills with
@@ -40,7 +40,7 @@ def bf16_bits(t):
 
 
 @pytest.mark.parametrize("H,D,M,cached,S,start", [
-    (32, 128, 3000, 256, 512, 2900),  # BASELINE config 3 shape, wrapped window
+    (32, 128, 3000, 256, 512, 2900),  # 512 new rows after 256 cached, wrapped window
     (4, 64, 300, 100, 130, 250),      # head_dim 64, ragged last q-tile, wraps
     (2, 128, 1000, 0, 65, 990),       # empty cache before the chunk
     (3, 64, 200, 17, 1, 190),         # single query

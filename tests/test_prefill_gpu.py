@@ -1,4 +1,5 @@
-"""Chunked causal prefill on the GPU against the oracle.
+"""Chunked causal prefill on the GPU (512 new rows after 256 cached, 32 x 128,
+and smaller cases) against the oracle.
 
 f32 variant within 1e-4 of the oracle; bf16-MFMA variant within 2e-2 (the
 north star's bars); the split-bf16 variant (three bf16 products per f32
@@ -58,7 +59,7 @@ def test_prefill_fixtures(gpu, name):
 
 
 @pytest.mark.parametrize("H,D,M,cached,S,start", [
-    (32, 128, 3000, 256, 512, 2900),  # BASELINE config 3 shape, wrapped window
+    (32, 128, 3000, 256, 512, 2900),  # 512 new rows after 256 cached, wrapped window
     (4, 128, 300, 0, 300, 0),         # empty cache, full ring
     (3, 64, 200, 17, 1, 190),         # single query == decode
     (2, 128, 1000, 100, 65, 950),     # ragged last q-tile
