@@ -21,17 +21,17 @@
 // bit.
 //
 // Rows are dealt to groups of KP waves (KP = 1 up to K = 4096): group g owns
-// the contiguous rows g*R .. g*R + R-1 (R <= 12), with two rows in flight:
-// row j + 2 is requested as soon as row j is reduced, and the first two
-// before x is staged.  The KP waves of a group keep their partial sums and
-// combine through LDS once, at the end.  K <= 4096: eight waves per CU in
-// workgroups of four; K > 4096: one workgroup of 12 waves per CU, so that x
-// is staged once per CU.  Measured per projection shape against the
-// alternatives: three to twelve rows in flight, four, twelve or sixteen
-// waves per CU at K <= 4096, rows dealt round-robin over the waves, and
-// nontemporal weight loads were all slower (the last by up to 15% on the
-// FFN's linear_in: the three loads of a row share cache lines, which plain
-// loads let the CU's cache serve).
+// the contiguous rows g*R .. g*R + R-1 (R <= 12), one row ahead: row j + 1
+// is requested just before row j is reduced, and row 0 before x is staged.
+// The KP waves of a group keep their partial sums and combine through LDS
+// once, at the end.  K <= 4096: eight waves per CU in workgroups of four;
+// K > 4096: one workgroup of 12 waves per CU, so that x is staged once per
+// CU.  Measured per projection shape against the alternatives: rows requested
+// two to twelve ahead (or two ahead, after the reduction), four, six,
+// twelve or sixteen waves per CU at K <= 4096, rows dealt round-robin over
+// the waves, and nontemporal weight loads were all slower (the last by up to
+// 15% on the FFN's linear_in: the three loads of a row share cache lines,
+// which plain loads let the CU's cache serve).
 //
 // HBM-bound: 0.5625 bytes and 2 flops per weight (x and y are negligible).
 #include <algorithm>
@@ -94,10 +94,8 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // Group g of the grid owns the contiguous rows g*R .. g*R + R-1; its KP
 // waves cover slots 64*kp + lane of each of them (KP = 1 up to K = 4096),
-// with two rows in flight, and keep their partial sums until the end, where
-// the KP waves of a group combine through LDS once.  G groups per
-// workgroup.
-constexpr int kRowsInFlight = 2;
+// one row ahead, and keep their partial sums until the end, where the KP
+// waves of a group combine through LDS once.  G groups per workgroup.
 
 template <int R, int KP, int G>
 __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kParams p) {
@@ -120,7 +118,7 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kP
   const uint8_t* wslot = p.w + (size_t)blk * kQ4kBlockBytes + 16 + 32 * it;
   const uint8_t* whead = p.w + (size_t)blk * kQ4kBlockBytes;
 
-  // x is requested first, then the first rows, so that waiting for x does
+  // x is requested first, then the first row, so that waiting for x does
   // not wait for the weights.  The workgroup stages x in LDS, slot c at row c
   // of pitch 68 floats (the 16 lanes of a read phase then hit distinct
   // banks), and each lane copies its slot into registers.
@@ -151,9 +149,7 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kP
     qa[j] = ld16(wslot + off);
     qb[j] = ld16(wslot + off + 16);
   };
-  constexpr int D = kRowsInFlight < R ? kRowsInFlight : R;
-#pragma unroll
-  for (int j = 0; j < D; ++j) load(j);
+  load(0);
   __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -188,8 +184,9 @@ __global__ __launch_bounds__(64 * KP * G) void q4k_matvec_rows_kernel(const Q4kP
   float acc[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) {
+    // Row j + 1 is requested before row j is reduced.
+    if (j + 1 < R) load(j + 1);
     acc[j] = wave_sum(slot_dot(hd[j], qa[j], qb[j], 2 * it, xv, sxl, sxh));
-    if (j + D < R) load(j + D);
   }
   auto store = [&](int j, float v) {
     const uint32_t row = row0 + j;
