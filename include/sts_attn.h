@@ -475,8 +475,9 @@ int sts_embed_add_q4_0(const uint8_t* table, uint32_t vocab, const uint32_t* tok
  * penalty tokens ptoks[b*pt_stride ..] (num_penalty[b*rs_stride] of them, at
  * most 30), token to out[b*out_stride].  top_k <= 1 is the argmax.
  * vocab <= 4096, top_k <= 256.  The top k and their order equal the
- * shader's for distinct logits (among equal logits this build ranks lower
- * indices first); the softmax sum and running total are summed in a
+ * shader's for distinct logits (among equal logits, -0 and +0 included, this
+ * build ranks lower indices first); the softmax sum and running total are
+ * summed in a
  * different f32 order, so the draw can differ only where rand lies within
  * rounding of a cumulative boundary.
  */

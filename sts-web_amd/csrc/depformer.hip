@@ -270,185 +270,282 @@ __global__ __launch_bounds__(256) void embed_add_kernel(const uint8_t* __restric
   h[(size_t)b * D + e] = proj[(size_t)b * D + e] + emb;
 }
 
-// Monotone map of a float to a uint32 (larger float -> larger key).
+// Monotone map of a float to a uint32 (larger float -> larger key), and back.
 __device__ __forceinline__ uint32_t order_key(float v) {
   const uint32_t u = __builtin_bit_cast(uint32_t, v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
+// row (DPP row_shr 1, 2, 4, 8), then the row totals carried across rows by
+// the GFX9 row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2
+// and 3).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
+// The value of lane ^ MASK (MASK < 64).
+template <int MASK>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  if constexpr (MASK == 1)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  else if constexpr (MASK == 2)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  else if constexpr (MASK < 32)
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (MASK << 10));  // bitmask mode, xor
+  else
+    return (uint32_t)__shfl_xor((int)x, MASK, 64);
+}
+
+// Bitonic sort of 256 64-bit keys, one per thread of the workgroup, into
+// descending order (thread t ends with the key of rank t).  Partners inside a
+// wave are reached by lane exchanges; the three steps whose partner is in
+// another wave (strides 64 and 128) go through `buf` (2 x 256 keys).
+template <int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_steps(uint64_t& x, uint32_t t, uint64_t* buf, int& half) {
+  uint64_t y;
+  if constexpr (STRIDE >= 64) {
+    uint64_t* b = buf + 256 * half;
+    half ^= 1;
+    b[t] = x;
+    __syncthreads();
+    y = b[t ^ STRIDE];
+  } else {
+    const uint32_t lo = lane_xor<STRIDE>((uint32_t)x), hi = lane_xor<STRIDE>((uint32_t)(x >> 32));
+    y = ((uint64_t)hi << 32) | lo;
+  }
+  // The lower partner of a pair keeps the larger key in blocks that sort
+  // descending (t & SIZE clear), the smaller one in blocks that sort ascending.
+  const bool keep_max = ((t & STRIDE) == 0) == ((t & SIZE) == 0);
+  x = (keep_max ? y > x : y < x) ? y : x;
+  if constexpr (STRIDE > 1) bitonic_steps<SIZE, STRIDE / 2>(x, t, buf, half);
+}
+// The three LDS steps alternate between the halves of `buf`, so a step's
+// stores never meet the previous step's loads (one barrier lies between).
+template <int SIZE>
+__device__ __forceinline__ void bitonic_sort256(uint64_t& x, uint32_t t, uint64_t* buf, int& half) {
+  bitonic_steps<SIZE, SIZE / 2>(x, t, buf, half);
+  if constexpr (SIZE < 256) bitonic_sort256<SIZE * 2>(x, t, buf, half);
+}
 
 // shader_sample_topk.wgsl for one stream per workgroup.  Penalty, temperature
-// and the argmax follow the shader's lanes and tree exactly.  The top K are
-// found by a radix select of the K-th largest value and ranked by counting
-// (value descending, ties by index), which for distinct values is the
-// shader's selection and insertion sort; the softmax values are the shader's
-// (exp of v - max), their sum and running total come from a wave scan.
+// and (top_k <= 1) the argmax follow the shader's lanes and tree exactly.  The
+// top K are found by a radix select of the K-th largest value and ranked by
+// a bitonic sort of (value descending, index ascending) keys, which for
+// distinct values is the shader's selection and insertion sort; the softmax
+// values are the shader's (exp of v - max), their sum and running total come
+// from a wave scan.  Thread t holds logits t, t + 256, ... in registers: NJ
+// of them, NJ * 256 >= V.
+template <int NJ>
 __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) {
-  __shared__ float vals[kMaxVocab];
+  __shared__ float vals[NJ * 256];
   __shared__ float tv[256];
   __shared__ uint32_t ti[256];
-  __shared__ uint32_t hist[256];
-  __shared__ float sv[kMaxTopK], ev[kMaxTopK];
-  __shared__ uint32_t si[kMaxTopK];
-  __shared__ float rv[kMaxTopK];
+  __shared__ __align__(16) uint32_t hist[3][256];
+  __shared__ uint32_t s_cnt[2][64];
+  __shared__ __align__(16) float ev[kMaxTopK];
   __shared__ uint32_t ri[kMaxTopK];
-  __shared__ uint32_t s_digit, s_rem, s_count, s_eq;
+  __shared__ float s_maxv;
   __shared__ uint32_t s_ptok[kMaxPenalty];
-  __shared__ uint64_t ck[kMaxTopK];
+  __shared__ uint64_t sbuf[2 * kMaxTopK];
+  static_assert(kMaxTopK == 256, "one key per thread in the ranking sort");
   const uint32_t tid = threadIdx.x, b = blockIdx.x, V = p.V;
+  const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float* lg = p.logits + (size_t)b * p.ld_logits;
-  for (uint32_t i = tid; i < V; i += 256) vals[i] = lg[i];
-  __syncthreads();
+
+  // The logits and the penalty list are requested together.
+  const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
+  float x[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t i = tid + 256u * j;
+    x[j] = i < V ? lg[i] : 0.f;
+  }
+  const uint32_t tok = tid < np ? p.ptoks[(size_t)b * p.pt_stride + tid] : 0u;
+  hist[0][tid] = 0;
+  hist[1][tid] = 0;
 
   // Repetition penalty (:56-69); a token listed twice is penalised once.
-  const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
-  if (tid < np) s_ptok[tid] = p.ptoks[(size_t)b * p.pt_stride + tid];
-  __syncthreads();
-  if (tid < np) {
-    const uint32_t tok = s_ptok[tid];
-    bool dup = false;
-    for (uint32_t q = 0; q < tid; ++q) dup |= s_ptok[q] == tok;
-    if (!dup && tok < V) {
-      const float v = vals[tok];
-      vals[tok] = v > 0.f ? v / p.penalty : v * p.penalty;
+  if (np > 0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t i = tid + 256u * j;
+      if (i < V) vals[i] = x[j];
     }
-  }
-  __syncthreads();
-
-  // Temperature and per-lane maxima (:72-88), tree argmax (:95-106).
-  float lmax = -3.402823466e+38f;
-  uint32_t lidx = 0;
-  for (uint32_t i = tid; i < V; i += 256) {
-    const float v = vals[i] / p.temperature;
-    vals[i] = v;
-    if (v > lmax) {
-      lmax = v;
-      lidx = i;
-    }
-  }
-  tv[tid] = lmax;
-  ti[tid] = lidx;
-  __syncthreads();
-  for (uint32_t half = 128; half > 0; half >>= 1) {
-    if (tid < half && tv[tid + half] > tv[tid]) {
-      tv[tid] = tv[tid + half];
-      ti[tid] = ti[tid + half];
+    if (tid < np) s_ptok[tid] = tok;
+    __syncthreads();
+    if (tid < np) {
+      bool dup = false;
+      for (uint32_t q = 0; q < tid; ++q) dup |= s_ptok[q] == tok;
+      if (!dup && tok < V) {
+        const float v = vals[tok];
+        vals[tok] = v > 0.f ? v / p.penalty : v * p.penalty;
+      }
     }
     __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t i = tid + 256u * j;
+      if (i < V) x[j] = vals[i];
+    }
   }
+  // Temperature (:72-88).
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) x[j] = x[j] / p.temperature;
+
   uint32_t* outp = p.out + (size_t)b * p.out_stride;
   const uint32_t K = p.top_k;
   if (K <= 1) {
+    // Per-lane maxima and the tree argmax (:95-106), first index on ties
+    // within a lane.
+    float lmax = -3.402823466e+38f;
+    uint32_t lidx = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t i = tid + 256u * j;
+      if (i < V && x[j] > lmax) {
+        lmax = x[j];
+        lidx = i;
+      }
+    }
+    tv[tid] = lmax;
+    ti[tid] = lidx;
+    __syncthreads();
+    for (uint32_t half = 128; half > 0; half >>= 1) {
+      if (tid < half && tv[tid + half] > tv[tid]) {
+        tv[tid] = tv[tid + half];
+        ti[tid] = ti[tid + half];
+      }
+      __syncthreads();
+    }
     if (tid == 0) *outp = ti[0];
     return;
   }
 
-  // Radix select of the Ks-th largest key, 8 bits at a time from the top.
+  // -0 takes the key of +0: the two compare equal as floats, so they tie
+  // (and go by index) as in a float comparison.
+  uint32_t k[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) k[j] = order_key(x[j] == 0.f ? 0.f : x[j]);
+  __syncthreads();  // histograms cleared
+
+  // Radix select of the Ks-th largest key, 8 bits at a time from the top,
+  // stopping early once the bin holding it is taken whole.  Every wave picks
+  // the digit itself from the histogram (one barrier per pass); the three
+  // histograms rotate, pass p clearing the one pass p + 2 counts into, whose
+  // last reads (pass p - 1) all precede this pass's barrier.
   const uint32_t Ks = min(K, V);
   uint32_t prefix = 0, mask = 0, rem = Ks;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    hist[tid] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < V; i += 256) {
-      const uint32_t k = order_key(vals[i]);
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 0xFFu], 1u);
-    }
-    __syncthreads();
-    if (tid < 64) {
-      // Wave 0 picks the digit: lane l holds bins 4l..4l+3; a suffix sum over
-      // lanes finds the lane whose bins straddle the rem-th largest key.
-      const uint32_t h0 = hist[4 * tid], h1 = hist[4 * tid + 1], h2 = hist[4 * tid + 2],
-                     h3 = hist[4 * tid + 3];
-      uint32_t suf = h0 + h1 + h2 + h3;
+    uint32_t* H = hist[pass % 3];
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t v = __shfl_down(suf, off, 64);
-        if (tid + off < 64) suf += v;
-      }
-      uint32_t above = __shfl_down(suf, 1, 64);  // keys in higher lanes' bins
-      if (tid == 63) above = 0;
-      if (suf >= rem && above < rem) {
-        const uint32_t hb[4] = {h0, h1, h2, h3};
-        uint32_t cum = above;
-        for (int d = 3; d >= 0; --d) {
-          if (cum + hb[d] >= rem) {
-            s_digit = 4 * tid + d;
-            s_rem = rem - cum;
-            break;
-          }
-          cum += hb[d];
-        }
-      }
+    for (int j = 0; j < NJ; ++j) {
+      if (tid + 256u * j < V && (k[j] & mask) == prefix) atomicAdd(&H[(k[j] >> shift) & 0xFFu], 1u);
     }
     __syncthreads();
-    prefix |= s_digit << shift;
+    // Lane l holds bins 4g .. 4g+3 with g = 63 - l, so the lane prefix sum
+    // counts the keys in bins >= 4g; the lane whose bins straddle the
+    // rem-th largest key has above < rem <= incl.
+    const uint32_t g = 63u - lane;
+    const uint4 hb = *reinterpret_cast<const uint4*>(&H[4 * g]);
+    const uint32_t own = hb.x + hb.y + hb.z + hb.w;
+    const uint32_t incl = wave_scan_incl(own);
+    const uint32_t above = incl - own;
+    const uint32_t h[4] = {hb.x, hb.y, hb.z, hb.w};
+    uint32_t cum = above, dig = 0, nrem = 0, exact = 0;
+    bool found = false;
+#pragma unroll
+    for (int d = 3; d >= 0; --d) {
+      const bool here = !found && cum + h[d] >= rem;
+      dig = here ? 4 * g + d : dig;
+      nrem = here ? rem - cum : nrem;
+      exact = here ? (uint32_t)(h[d] == rem - cum) : exact;
+      found |= here;
+      cum += h[d];
+    }
+    // Read with every lane active (the source lane must hold its values).
+    const uint64_t hit = __ballot(above < rem && incl >= rem);
+    const int src = (int)__builtin_ctzll(hit);
+    const uint32_t digit = __builtin_amdgcn_readlane(dig, src);
+    rem = __builtin_amdgcn_readlane(nrem, src);
+    const uint32_t ex = __builtin_amdgcn_readlane(exact, src);
+    hist[(pass + 2) % 3][tid] = 0;
+    prefix |= digit << shift;
     mask |= 0xFFu << shift;
-    rem = s_rem;
+    if (ex) break;
   }
-  // Keys above the threshold are all taken; of those equal to it, `rem`.
-  if (tid == 0) {
-    s_count = 0;
-    s_eq = 0;
-  }
-  __syncthreads();
-  for (uint32_t i = tid; i < V; i += 256) {
-    const uint32_t k = order_key(vals[i]);
-    if (k > prefix) {
-      const uint32_t slot = atomicAdd(&s_count, 1u);
-      sv[slot] = vals[i];
-      si[slot] = i;
-    } else if (k == prefix) {
-      atomicAdd(&s_eq, 1u);
+
+  // Collection in index order: keys above the threshold prefix all, of those
+  // on it the first `rem` (all of them when the bin was taken whole).  Slots
+  // come from per-(j, wave) ballot counts, so the order is deterministic.
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const bool valid = tid + 256u * j < V;
+    const uint64_t bg = __ballot(valid && (k[j] & mask) > prefix);
+    const uint64_t be = __ballot(valid && (k[j] & mask) == prefix);
+    if (lane == 0) {
+      s_cnt[0][4 * j + wave] = (uint32_t)__builtin_popcountll(bg);
+      s_cnt[1][4 * j + wave] = (uint32_t)__builtin_popcountll(be);
     }
   }
   __syncthreads();
-  if (s_eq == rem) {
-    for (uint32_t i = tid; i < V; i += 256)
-      if (order_key(vals[i]) == prefix) {
-        const uint32_t slot = atomicAdd(&s_count, 1u);
-        sv[slot] = vals[i];
-        si[slot] = i;
-      }
-  } else if (tid == 0) {
-    // Ties at the threshold: the lowest indices.
-    uint32_t c = s_count, take = rem;
-    for (uint32_t i = 0; i < V && take > 0; ++i)
-      if (order_key(vals[i]) == prefix) {
-        sv[c] = vals[i];
-        si[c] = i;
-        ++c;
-        --take;
-      }
-  }
-  __syncthreads();
-  // Rank by counting: value descending, index ascending, as one 64-bit key
-  // (order key above, complemented index below) so the count is branch-free.
-  if (tid < Ks) ck[tid] = ((uint64_t)order_key(sv[tid]) << 32) | (0xFFFFFFFFu - si[tid]);
-  __syncthreads();
-  if (tid < Ks) {
-    const uint64_t mine = ck[tid];
-    uint32_t rank = 0;
-    uint32_t j = 0;
-    for (; j + 8 <= Ks; j += 8) {
-      uint64_t c[8];
+  // Entries past 4 * NJ are never written: they count nothing.
+  const uint32_t cg = lane < 4u * NJ ? s_cnt[0][lane] : 0u;
+  const uint32_t ce = lane < 4u * NJ ? s_cnt[1][lane] : 0u;
+  const uint32_t ig = wave_scan_incl(cg), ie = wave_scan_incl(ce);
+  const uint32_t xg = ig - cg, xe = ie - ce;  // exclusive prefix over (j, wave)
+  const uint32_t total_g = __builtin_amdgcn_readlane(ig, 63);
+  uint64_t* ck = sbuf;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) c[u] = ck[j + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) rank += c[u] > mine ? 1u : 0u;
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t i = tid + 256u * j;
+    const bool valid = i < V;
+    const bool gt = valid && (k[j] & mask) > prefix, eq = valid && (k[j] & mask) == prefix;
+    const uint64_t bg = __ballot(gt), be = __ballot(eq);
+    // The bases are read with every lane active: inside the divergent branch
+    // below, the source lane 4j + wave may be inactive, and the compiler is
+    // free to compute xg / xe there for the active lanes only.
+    const uint32_t gbase = __builtin_amdgcn_readlane(xg, 4 * j + wave);
+    const uint32_t ebase = __builtin_amdgcn_readlane(xe, 4 * j + wave);
+    const uint64_t key = ((uint64_t)k[j] << 32) | (0xFFFFFFFFu - i);
+    if (gt) {
+      const uint32_t slot = gbase + __builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(bg >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bg, 0u));
+      if (slot < kMaxTopK) ck[slot] = key;
+    } else if (eq) {
+      const uint32_t e = ebase + __builtin_amdgcn_mbcnt_hi(
+                                     (uint32_t)(be >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)be, 0u));
+      if (e < rem && total_g + e < kMaxTopK) ck[total_g + e] = key;
     }
-    for (; j < Ks; ++j) rank += ck[j] > mine ? 1u : 0u;
-    rv[rank] = sv[tid];
-    ri[rank] = si[tid];
   }
+  // Slots past the Ks taken hold 0, below every real key (the index part of
+  // a real key is at least 2^32 - kMaxVocab).
+  if (tid >= Ks) ck[tid] = 0;
+  __syncthreads();
+
+  // Rank: value descending, index ascending.
+  uint64_t key = ck[tid];
+  int half = 0;
+  bitonic_sort256<2>(key, tid, sbuf, half);
   // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
-  for (uint32_t j = Ks + tid; j < K; j += 256) {
-    rv[j] = -3.402823466e+38f;
-    ri[j] = 0;
-  }
+  const bool real = tid < Ks;
+  const float v = real ? key_value((uint32_t)(key >> 32)) : -3.402823466e+38f;
+  ri[tid] = real ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+  if (tid == 0) s_maxv = v;
   __syncthreads();
   // Softmax over the K (:198-210) and the cumulative draw (:212-221).
-  const float max_v = rv[0];
-  for (uint32_t j = tid; j < K; j += 256) ev[j] = expf(rv[j] - max_v);
+  const float max_v = s_maxv;
+  if (tid < K) ev[tid] = expf(v - max_v);
   __syncthreads();
   if (tid < 64) {
     // Wave 0: lane l holds values 4l..4l+3.  The sum and the running total
@@ -471,8 +568,8 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
     float pre = run;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const float v = __shfl_up(pre, off, 64);
-      if (tid >= off) pre += v;
+      const float w = __shfl_up(pre, off, 64);
+      if (tid >= off) pre += w;
     }
     pre -= run;
     const float rnd = p.rand[(size_t)b * p.rs_stride];
@@ -601,7 +698,10 @@ int launch_sample_topk(const SampleParams& p, hipStream_t stream) {
   if (p.top_k > kMaxTopK)
     return fail(STS_ERR_INVALID, "top_k %u exceeds %u", p.top_k, kMaxTopK);
   if (p.B == 0) return STS_OK;
-  hipLaunchKernelGGL(sample_topk_kernel, dim3(p.B), dim3(256), 0, stream, p);
+  if (p.V <= 2048)
+    hipLaunchKernelGGL(sample_topk_kernel<8>, dim3(p.B), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(sample_topk_kernel<16>, dim3(p.B), dim3(256), 0, stream, p);
   STS_HIP(hipGetLastError());
   return STS_OK;
 }

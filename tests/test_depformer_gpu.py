@@ -164,6 +164,68 @@ def test_sample_topk_against_oracle(gpu, V, K):
     assert checked >= B - 2
 
 
+def _sample_ties(logits, top_k, temp, penalty, rand, ptoks):
+    """The kernel's rule where values repeat: the top k by value descending,
+    ties by index ascending (so the k-th largest value's ties go to the lowest
+    indices), then the cumulative draw.  Returns (token, safe): safe is False
+    when rand lies within 1e-5 of a cumulative boundary."""
+    lg = np.array(logits, np.float32)
+    for t in dict.fromkeys(int(t) for t in ptoks):
+        if t < lg.size:
+            lg[t] = lg[t] / np.float32(penalty) if lg[t] > 0 else lg[t] * np.float32(penalty)
+    lg = lg / np.float32(temp)
+    srt = np.argsort(-lg.astype(np.float64), kind="stable")
+    k = min(top_k, lg.size)
+    v = np.full(top_k, -3.402823466e+38)
+    v[:k] = lg[srt[:k]]
+    p = np.exp(v - v[0])
+    cum = np.cumsum(p / p.sum())
+    j = min(int(np.searchsorted(cum, rand, side="right")), top_k - 1)
+    tok = int(srt[j]) if j < k else 0
+    return tok, bool(np.min(np.abs(cum - rand)) > 1e-5)
+
+
+@pytest.mark.parametrize("V,K", [(2048, 250), (2048, 256), (2048, 20), (2048, 1), (300, 2),
+                                 (100, 150), (4096, 250)])
+def test_sample_topk_ties(gpu, V, K):
+    """Logits on a coarse grid, so values repeat and the k-th largest is
+    tied: rows with every value equal, rows with two values, a row of -0 and
+    +0 (equal as floats), rows on a 0.25 grid.  top_k > 1 follows the ranking rule above; top_k = 1 the shader's
+    lane and tree argmax (the oracle), whose choice among equal maxima is
+    not the lowest index."""
+    B = 24
+    rng = np.random.default_rng(V * 13 + K)
+    logits = (np.round(rng.standard_normal((B, V)) * 4) / 4).astype(np.float32)
+    logits[0:3] = np.float32(0.5)
+    logits[3] = np.float32(-1.0)
+    logits[3, 7::9] = np.float32(2.0)
+    logits[4] = np.float32(1.0)
+    logits[4, ::2] = np.float32(-2.0)
+    logits[5] = np.float32(-0.0)                         # -0 and +0 tie
+    logits[5, ::3] = np.float32(0.0)
+    logits[5, 10] = np.float32(1.0)
+    rand = rng.random(B).astype(np.float32)
+    rand[0] = np.float32(0.0)
+    rand[1] = np.float32(0.999)
+    pt = rng.integers(0, V, size=(B, 30)).astype(np.uint32)
+    npn = rng.integers(0, 31, size=B).astype(np.uint32)
+    npn[:6] = 0
+    got = host(sts_attn.sample_top_k(dev(logits), K, 0.8, 1.3, dev(rand), dev(pt.view(np.int32)),
+                                     dev(npn.view(np.int32)))).view(np.uint32)
+    checked = 0
+    for b in range(B):
+        if K <= 1:
+            want, _ = oracle.sample_topk_wgsl(logits[b], K, 0.8, 1.3, float(rand[b]),
+                                              pt[b, :npn[b]])
+            safe = True
+        else:
+            want, safe = _sample_ties(logits[b], K, 0.8, 1.3, float(rand[b]), pt[b, :npn[b]])
+        if safe:
+            assert got[b] == want, (b, got[b], want)
+            checked += 1
+    assert checked >= B - 3
+
+
 def _inputs(cfg, B, seed):
     S = cfg["num_steps"]
     th = oracle.normal(seed, (B, cfg["temporal_dim"]))
