@@ -293,54 +293,70 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
   return v;
 }
 
-// The value of lane ^ MASK (MASK < 64).
+// The value of lane ^ MASK (MASK < 16): quad permutations on DPP, the
+// ds_swizzle bitmask mode (xor) above that.
 template <int MASK>
 __device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
   if constexpr (MASK == 1)
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   else if constexpr (MASK == 2)
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-  else if constexpr (MASK < 32)
-    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (MASK << 10));  // bitmask mode, xor
   else
-    return (uint32_t)__shfl_xor((int)x, MASK, 64);
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1F | (MASK << 10));
 }
 
-// Bitonic sort of 256 64-bit keys, one per thread of the workgroup, into
-// descending order (thread t ends with the key of rank t).  Partners inside a
-// wave are reached by lane exchanges; the three steps whose partner is in
-// another wave (strides 64 and 128) go through `buf` (2 x 256 keys).
+// Bitonic sort of 64 64-bit keys, one per lane, into descending order (lane l
+// ends with the wave's key of rank l).  Partners at lane distance 16 and 32
+// come from the gfx950 permlane swaps, which return the lane's own key and
+// its partner's in a lane-dependent order: the compare-exchange takes the
+// larger or smaller of the two, which does not depend on that order.
 template <int SIZE, int STRIDE>
-__device__ __forceinline__ void bitonic_steps(uint64_t& x, uint32_t t, uint64_t* buf, int& half) {
-  uint64_t y;
-  if constexpr (STRIDE >= 64) {
-    uint64_t* b = buf + 256 * half;
-    half ^= 1;
-    b[t] = x;
-    __syncthreads();
-    y = b[t ^ STRIDE];
+__device__ __forceinline__ void wave_bitonic_steps(uint64_t& x, uint32_t lane) {
+  // The lower partner of a pair keeps the larger key in blocks that sort
+  // descending (lane & SIZE clear), the smaller one in blocks that sort
+  // ascending.
+  const bool keep_max = ((lane & STRIDE) == 0) == ((lane & SIZE) == 0);
+  if constexpr (STRIDE >= 16) {
+    const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+    const auto l2 = STRIDE == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                                 : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h2 = STRIDE == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                                 : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const uint64_t a = ((uint64_t)h2[0] << 32) | l2[0], c = ((uint64_t)h2[1] << 32) | l2[1];
+    const uint64_t mx = a > c ? a : c, mn = a > c ? c : a;
+    x = keep_max ? mx : mn;
   } else {
     const uint32_t lo = lane_xor<STRIDE>((uint32_t)x), hi = lane_xor<STRIDE>((uint32_t)(x >> 32));
-    y = ((uint64_t)hi << 32) | lo;
+    const uint64_t y = ((uint64_t)hi << 32) | lo;
+    x = (keep_max ? y > x : y < x) ? y : x;
   }
-  // The lower partner of a pair keeps the larger key in blocks that sort
-  // descending (t & SIZE clear), the smaller one in blocks that sort ascending.
-  const bool keep_max = ((t & STRIDE) == 0) == ((t & SIZE) == 0);
-  x = (keep_max ? y > x : y < x) ? y : x;
-  if constexpr (STRIDE > 1) bitonic_steps<SIZE, STRIDE / 2>(x, t, buf, half);
+  if constexpr (STRIDE > 1) wave_bitonic_steps<SIZE, STRIDE / 2>(x, lane);
 }
-// The three LDS steps alternate between the halves of `buf`, so a step's
-// stores never meet the previous step's loads (one barrier lies between).
 template <int SIZE>
-__device__ __forceinline__ void bitonic_sort256(uint64_t& x, uint32_t t, uint64_t* buf, int& half) {
-  bitonic_steps<SIZE, SIZE / 2>(x, t, buf, half);
-  if constexpr (SIZE < 256) bitonic_sort256<SIZE * 2>(x, t, buf, half);
+__device__ __forceinline__ void wave_bitonic_sort(uint64_t& x, uint32_t lane) {
+  wave_bitonic_steps<SIZE, SIZE / 2>(x, lane);
+  if constexpr (SIZE < 64) wave_bitonic_sort<SIZE * 2>(x, lane);
+}
+
+// Number of keys of the descending list L[0..64) above x (STRICT) or at or
+// above x: a branch-free binary search, 6 halving steps and a last check.
+template <bool STRICT>
+__device__ __forceinline__ uint32_t count_above(const uint64_t* L, uint64_t x) {
+  uint32_t pos = 0;
+#pragma unroll
+  for (uint32_t step = 32; step >= 1; step >>= 1) {
+    const uint64_t y = L[pos + step - 1];
+    pos += (STRICT ? y > x : y >= x) ? step : 0u;
+  }
+  const uint64_t y = L[pos];  // pos <= 63 here
+  return pos + ((STRICT ? y > x : y >= x) ? 1u : 0u);
 }
 
 // shader_sample_topk.wgsl for one stream per workgroup.  Penalty, temperature
 // and (top_k <= 1) the argmax follow the shader's lanes and tree exactly.  The
 // top K are found by a radix select of the K-th largest value and ranked by
-// a bitonic sort of (value descending, index ascending) keys, which for
+// (value descending, index ascending) keys -- per-wave bitonic sorts merged
+// by binary-search ranks -- which for
 // distinct values is the shader's selection and insertion sort; the softmax
 // values are the shader's (exp of v - max), their sum and running total come
 // from a wave scan.  Thread t holds logits t, t + 256, ... in registers: NJ
@@ -533,10 +549,25 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   if (tid >= Ks) ck[tid] = 0;
   __syncthreads();
 
-  // Rank: value descending, index ascending.
+  // Rank: value descending, index ascending.  Each wave sorts its 64 keys;
+  // a key's rank is its place in its wave's list plus the keys above it in
+  // the other three lists (equal keys, the padding zeros, count as above
+  // when they are in a lower wave, so the ranks are distinct).
   uint64_t key = ck[tid];
-  int half = 0;
-  bitonic_sort256<2>(key, tid, sbuf, half);
+  wave_bitonic_sort<2>(key, lane);
+  uint64_t* lists = sbuf;  // each thread overwrites only the slot it read
+  lists[tid] = key;
+  __syncthreads();
+  uint32_t rank = lane;
+#pragma unroll
+  for (uint32_t i = 1; i < 4; ++i) {
+    const uint32_t w2 = (wave + i) & 3u;
+    rank += w2 > wave ? count_above<true>(lists + 64 * w2, key)
+                      : count_above<false>(lists + 64 * w2, key);
+  }
+  sbuf[256 + rank] = key;
+  __syncthreads();
+  key = sbuf[256 + tid];
   // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
   const bool real = tid < Ks;
   const float v = real ? key_value((uint32_t)(key >> 32)) : -3.402823466e+38f;
