@@ -355,11 +355,10 @@ __device__ __forceinline__ uint32_t count_above(const uint64_t* L, uint64_t x) {
 // shader_sample_topk.wgsl for one stream per workgroup.  Penalty, temperature
 // and (top_k <= 1) the argmax follow the shader's lanes and tree exactly.  The
 // top K are found by a radix select of the K-th largest value and ranked by
-// (value descending, index ascending) keys -- per-wave bitonic sorts merged
-// by binary-search ranks -- which for
-// distinct values is the shader's selection and insertion sort; the softmax
-// values are the shader's (exp of v - max), their sum and running total come
-// from a wave scan.  Thread t holds logits t, t + 256, ... in registers: NJ
+// (value descending, index ascending) keys, per-wave bitonic sorts merged by
+// binary-search ranks, which for distinct values is the shader's selection
+// and insertion sort; the softmax values are the shader's (exp of v - max),
+// their sum and running total come from a wave scan.  Thread t holds logits t, t + 256, ... in registers: NJ
 // of them, NJ * 256 >= V.
 template <int NJ>
 __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) {
@@ -378,7 +377,8 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float* lg = p.logits + (size_t)b * p.ld_logits;
 
-  // The logits and the penalty list are requested together.
+  // The logits first; the penalty tokens once their count is in (only that
+  // many are guaranteed readable).
   const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
   float x[NJ];
 #pragma unroll
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
     }
     // Read with every lane active (the source lane must hold its values).
     const uint64_t hit = __ballot(above < rem && incl >= rem);
-    const int src = (int)__builtin_ctzll(hit);
+    const int src = hit ? (int)__builtin_ctzll(hit) : 0;  // one lane hits
     const uint32_t digit = __builtin_amdgcn_readlane(dig, src);
     rem = __builtin_amdgcn_readlane(nrem, src);
     const uint32_t ex = __builtin_amdgcn_readlane(exact, src);
