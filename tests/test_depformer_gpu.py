@@ -186,7 +186,8 @@ def _sample_ties(logits, top_k, temp, penalty, rand, ptoks):
 
 
 @pytest.mark.parametrize("V,K", [(2048, 250), (2048, 256), (2048, 20), (2048, 1), (300, 2),
-                                 (100, 150), (4096, 250)])
+                                 (100, 150), (4096, 250), (1, 2), (257, 256), (256, 256),
+                                 (2049, 250)])
 def test_sample_topk_ties(gpu, V, K):
     """Logits on a coarse grid, so values repeat and the k-th largest is
     tied: rows with every value equal, rows with two values, a row of -0 and
@@ -203,7 +204,7 @@ def test_sample_topk_ties(gpu, V, K):
     logits[4, ::2] = np.float32(-2.0)
     logits[5] = np.float32(-0.0)                         # -0 and +0 tie
     logits[5, ::3] = np.float32(0.0)
-    logits[5, 10] = np.float32(1.0)
+    logits[5, min(10, V - 1)] = np.float32(1.0)
     rand = rng.random(B).astype(np.float32)
     rand[0] = np.float32(0.0)
     rand[1] = np.float32(0.999)
