@@ -44,6 +44,11 @@ struct PrefillParams {
   // group_magic = ceil(2^32 / group), set by launch_prefill; 0 for group 1.
   uint32_t group = 1;
   uint32_t group_magic = 0;
+  // Start stagger of the bf16-mirror kernel, set by its launch when the grid
+  // fits in one round on the device: a query tile with fewer key blocks than
+  // the launch's longest sleeps start_stagger x ~128 clocks per block of
+  // difference before its first loads.  0: no stagger.
+  uint32_t start_stagger = 0;
 };
 
 // Checks everything launch_prefill would reject for these sizes, without
