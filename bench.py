@@ -40,7 +40,11 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 50 untimed steps: a fresh process's first kernels run slow for ~40-50
+    # steps (measured on the prefill: 27.9, 20.3, 19.8, 19.4 -> 19.2 us per
+    # layer over its first blocks of 10 steps), and a fresh allocation's
+    # first touches cost one more slow step.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--only", default="", help="comma list of sections to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
