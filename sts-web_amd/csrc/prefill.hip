@@ -26,6 +26,10 @@
 // Blocks are indexed (head, q-tile[, split]) with head fastest, so all
 // workgroups of a head land on the same XCD (workgroup id % 8) and share its
 // L2 copy of the head's K/V; the heaviest (last) q-tiles are dispatched first.
+// In prefill_ws_kernel (not its SPLIT instance) the tiles within two blocks
+// of the longest visit their key blocks last to first, ending on the blocks
+// every tile of the head shares (by then in L2); on the bf16-mirror path the
+// shorter tiles also start staggered when all tiles are resident at once.
 #include <algorithm>
 #include <cfloat>
 
