@@ -639,7 +639,9 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   // traffic; the shorter ones still finish first (measured at 512 queries
   // after 256 cached: 17.6 -> 16.5 us per layer).
   if (KV16 && p.start_stagger) {
-    const uint32_t n = (maxblk - nblk) * p.start_stagger;
+    // At most 16 blocks' worth: a bounded head start for the long tiles,
+    // however many blocks a launch has.
+    const uint32_t n = min(maxblk - nblk, 16u) * p.start_stagger;
     for (uint32_t i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(2);
   }
 
