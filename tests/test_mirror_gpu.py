@@ -44,6 +44,7 @@ def bf16_bits(t):
     (4, 64, 300, 100, 130, 250),      # head_dim 64, ragged last q-tile, wraps
     (2, 128, 1000, 0, 65, 990),       # empty cache before the chunk
     (3, 64, 200, 17, 1, 190),         # single query
+    (2, 128, 4096, 0, 2048, 4000),    # tiles of 1..32 blocks: start stagger at its cap
 ])
 def test_bf16kv_prefill_equals_f32_input(gpu, H, D, M, cached, S, start):
     q, kc, vc = prefill_inputs(6000 + S, H, D, M, cached, S, start)
