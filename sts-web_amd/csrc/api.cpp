@@ -80,6 +80,14 @@ int kv_ensure(sts_kv_cache* c, uint64_t batch, hipStream_t stream) {
     return STS_OK;
   }
   if (batch == 0) return fail(STS_ERR_INVALID, "batch must be >= 1");
+  // The lazy allocation must not be recorded into a HIP graph (its zero fill
+  // would be a memset node, and the graph would own nothing it addresses).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  STS_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(STS_ERR_STATE,
+                "the cache's first use allocates its buffers, which cannot happen while the "
+                "stream is being captured; allocate it first (sts_kv_ensure_allocated)");
   const uint64_t n = batch * c->heads * c->max_len * c->head_dim;
   if (hipMalloc(&c->k, n * sizeof(float)) != hipSuccess) {
     c->k = nullptr;
@@ -668,9 +676,21 @@ int sts_kv_prefill(sts_kv_cache* cache, const sts_rope* rope, const float* q,
               rope->max_seq_len);
   }
   hipStream_t s = as_stream(stream);
-  if (int rc = kv_ensure(cache, 1, s)) return rc;
   sts_kv_cache next = *cache;
   kv_advance(&next, seq);
+  const bool bf16_rows = precision == STS_PREC_BF16_MFMA && (cache->flags & STS_KV_BF16_MIRROR);
+  // Everything the attention launch needs is acquired before the append runs
+  // and the counters move: a call refused here (workspace needed while the
+  // stream is being captured, out of memory) leaves the cache as it was.
+  if (int rc = sts::reserve_prefill((uint32_t)seq, (uint32_t)cache->q_heads, (uint32_t)next.len,
+                                    (uint32_t)cache->head_dim, precision, bf16_rows, s))
+    return rc;
+  if (int rc = kv_ensure(cache, 1, s)) return rc;
+  next.k = cache->k;
+  next.v = cache->v;
+  next.k16 = cache->k16;
+  next.v16 = cache->v16;
+  next.batch = cache->batch;
   const uint32_t pos = (uint32_t)(cache->offset % cache->max_len);
   // RoPE of k (at offset + s) fused into one append launch of K and V.
   if (int rc = sts::launch_kv_append(k_new, v_new, cache->k, cache->v, pos, 1, (uint32_t)seq,

@@ -597,7 +597,26 @@ int scratch_address(hipStream_t stream, uint32_t** out) {
   return STS_OK;
 }
 
+// The split workspace of a launch planned for `units` (stream, head) pairs, or
+// null when the plan has one split.
+int decode_workspace(uint64_t units, uint32_t head_dim, const DecodePlan& pl, hipStream_t stream,
+                     Workspace** out) {
+  *out = nullptr;
+  if (pl.nsplit <= 1) return STS_OK;
+  // Partials and arrival counters.
+  return get_workspace(stream, (size_t)units * pl.nsplit * (padded_head_dim(head_dim) + 4), units,
+                       out);
+}
+
 }  // namespace
+
+int reserve_decode(uint32_t batch, uint32_t heads, uint32_t head_dim, uint32_t max_rows,
+                   hipStream_t stream) {
+  const uint64_t units = (uint64_t)batch * heads;
+  if (units == 0) return STS_OK;
+  Workspace* ws = nullptr;
+  return decode_workspace(units, head_dim, plan_decode(units, max_rows), stream, &ws);
+}
 
 int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
                   hipStream_t stream) {
@@ -605,12 +624,9 @@ int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t ma
   if (units == 0) return STS_OK;
   if (int rc = check_decode(p, batch, head_dim)) return rc;
   const DecodePlan pl = plan_decode(units, max_rows);
-  if (pl.nsplit > 1) {
-    // Partials and arrival counters.
-    Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)units * pl.nsplit * (padded_head_dim(head_dim) + 4),
-                                 units, &ws);
-    if (rc != STS_OK) return rc;
+  Workspace* ws = nullptr;
+  if (int rc = decode_workspace(units, head_dim, pl, stream, &ws)) return rc;
+  if (ws) {
     p.part = ws->part;
     p.counters = ws->counters;
   }

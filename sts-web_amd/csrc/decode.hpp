@@ -61,6 +61,12 @@ float softmax_scale_log2(float scale);
 int launch_decode(DecodeParams p, uint32_t batch, uint32_t head_dim, uint32_t max_rows,
                   hipStream_t stream);
 
+// Makes sure the split workspace that launch_decode needs for these sizes on
+// `stream` exists (allocating it now if not), so that a caller can fail before
+// it changes any state; launch_decode then finds it and cannot fail on it.
+int reserve_decode(uint32_t batch, uint32_t heads, uint32_t head_dim, uint32_t max_rows,
+                   hipStream_t stream);
+
 // launch_decode without allocating: the split records and arrival counters
 // live in a static device array of the library (8 MiB of records, 16384
 // counters per GPU); launches that need more fail with STS_ERR_INVALID.  All

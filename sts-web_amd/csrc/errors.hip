@@ -52,6 +52,14 @@ int device_error_word(uint32_t** word) {
 }
 
 int take_device_errors(hipStream_t stream, uint32_t* flags) {
+  // The swap must run now, not be recorded into a graph, and the stream must
+  // be waited for: neither is possible while it is being captured.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  STS_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(STS_ERR_STATE,
+                "the device error word cannot be read while the stream is being captured; "
+                "read it after the capture or the graph's replay");
   ErrorWords w;
   if (int rc = words_for_device(&w)) return rc;
   // Swapped to zero on the device after the work queued on `stream`, so no

@@ -1146,27 +1146,40 @@ int launch_ws(const PrefillParams& p, hipStream_t stream) {
   return STS_OK;
 }
 
+// Key-range splits of the f32 kernel: f32 tiles carry four times the MFMA
+// work of bf16 ones, so their key ranges are split until there are about two
+// workgroups per CU.
+uint32_t f32_splits(uint32_t S, uint32_t H) {
+  const uint32_t tiles = H * ((S + kBQ - 1) / kBQ);
+  const uint32_t cus = (uint32_t)device_cu_count();
+  const uint32_t nsplit = (2 * cus + tiles - 1) / tiles;
+  return std::max(1u, std::min<uint32_t>(nsplit, kMaxPrefillSplits));
+}
+
+// The split workspace of the f32 kernel (null with one split).
+template <int D>
+int f32_workspace(uint32_t S, uint32_t H, hipStream_t stream, uint32_t* nsplit, Workspace** out) {
+  *out = nullptr;
+  *nsplit = f32_splits(S, H);
+  if (*nsplit <= 1) return STS_OK;
+  const uint32_t tiles = H * ((S + kBQ - 1) / kBQ);
+  return get_workspace(stream, (size_t)tiles * *nsplit * 256 * (D / 4 + 2), tiles, out);
+}
+
 template <int D>
 int launch_f32(const PrefillParams& p, hipStream_t stream) {
   const uint32_t nqt = (p.S + kBQ - 1) / kBQ;
   if (nqt > 65535u) return fail(STS_ERR_INVALID, "seq %u too long for one launch", p.S);
   if ((uint64_t)p.M * D * sizeof(float) > 0x7FFFFFF0ull)
     return fail(STS_ERR_INVALID, "max_len %u too large for one head's buffer resource", p.M);
-  // f32 tiles carry four times the MFMA work of bf16 ones: split their key
-  // ranges until there are about two workgroups per CU.
-  const uint32_t tiles = p.H * nqt;
-  const uint32_t cus = (uint32_t)device_cu_count();
-  uint32_t nsplit = (2 * cus + tiles - 1) / tiles;
-  nsplit = std::max(1u, std::min<uint32_t>(nsplit, kMaxPrefillSplits));
   PrefillParams q = p;
-  q.nsplit = nsplit;
-  if (nsplit > 1) {
-    Workspace* ws = nullptr;
-    const int rc = get_workspace(stream, (size_t)tiles * nsplit * 256 * (D / 4 + 2), tiles, &ws);
-    if (rc != STS_OK) return rc;
+  Workspace* ws = nullptr;
+  if (int rc = f32_workspace<D>(p.S, p.H, stream, &q.nsplit, &ws)) return rc;
+  if (ws) {
     q.part = ws->part;
     q.counters = ws->counters;
   }
+  const uint32_t nsplit = q.nsplit;
   hipLaunchKernelGGL((prefill_kernel<D, kKsplit>), dim3(p.H, nqt, nsplit),
                      dim3(256 * kKsplit), 0, stream, q);
   STS_HIP(hipGetLastError());
@@ -1225,6 +1238,19 @@ static int launch_prefill_by_decode(const PrefillParams& p, uint32_t head_dim,
     d.rope_pos = p.rope_pos0;
   }
   return launch_decode(d, p.S, head_dim, p.len, stream);
+}
+
+int reserve_prefill(uint32_t S, uint32_t H, uint32_t len, uint32_t head_dim, int precision,
+                    bool bf16_rows, hipStream_t stream) {
+  uint32_t* err = nullptr;
+  if (int rc = device_error_word(&err)) return rc;
+  if (head_dim != 64 && head_dim != 128)
+    return reserve_decode(S, H, head_dim, len, stream);  // launch_prefill_by_decode's plan
+  if (bf16_rows || precision != STS_PREC_F32) return STS_OK;  // no workspace
+  uint32_t nsplit = 1;
+  Workspace* ws = nullptr;
+  return head_dim == 128 ? f32_workspace<128>(S, H, stream, &nsplit, &ws)
+                         : f32_workspace<64>(S, H, stream, &nsplit, &ws);
 }
 
 int launch_prefill(const PrefillParams& p0, uint32_t head_dim, int precision, hipStream_t stream) {

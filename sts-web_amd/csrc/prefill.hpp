@@ -58,5 +58,13 @@ int check_prefill(uint32_t seq, uint32_t heads, uint32_t head_dim, uint32_t max_
 
 int launch_prefill(const PrefillParams& p, uint32_t head_dim, int precision, hipStream_t stream);
 
+// Acquires, ahead of time, everything launch_prefill would acquire for these
+// sizes on `stream` (split workspace, device error word), so that a caller
+// that changes state before launching can fail first; afterwards
+// launch_prefill with the same sizes finds them and cannot fail on them.
+// bf16_rows: the launch will read bf16 copies of the caches.
+int reserve_prefill(uint32_t S, uint32_t H, uint32_t len, uint32_t head_dim, int precision,
+                    bool bf16_rows, hipStream_t stream);
+
 
 }  // namespace sts

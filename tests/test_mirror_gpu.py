@@ -131,3 +131,36 @@ def test_mirrored_prefill_equals_unmirrored(gpu):
     np.testing.assert_array_equal(host(va), host(vb))
     _check_mirror(a)
     assert sts_attn.device_errors() == 0
+
+
+def test_gqa_mirror_tracks_decode_steps(gpu):
+    """Grouped-query attention (32 query heads over 8 K/V heads) on a mirrored
+    cache: the appended row of a fused decode step is stored by the first query
+    head of its group, into the f32 cache and the mirror.  After chunk appends
+    and decode steps (B = 2, RoPE, a window that wraps) the mirror equals the
+    f32 cache rounded to bf16, bit for bit, and the attention output equals the
+    same steps on an unmirrored handle."""
+    Hq, Hkv, D, M, B = 32, 8, 128, 1000, 2
+    rope = sts_attn.RoPE(D, 8192)
+    a = sts_attn.KVCache(M, Hkv, D, bf16_mirror=True, n_heads=Hq)
+    b = sts_attn.KVCache(M, Hkv, D, n_heads=Hq)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    k0 = torch.randn((B, 990, Hkv, D), generator=g, device="cuda")
+    v0 = torch.randn((B, 990, Hkv, D), generator=g, device="cuda")
+    for c in (a, b):
+        c.advance(500)
+        c.update(k0, v0)
+    for step in range(24):  # crosses the ring's end at row 1000
+        q = torch.randn((B, Hq, D), generator=g, device="cuda")
+        k = torch.randn((B, Hkv, D), generator=g, device="cuda")
+        v = torch.randn((B, Hkv, D), generator=g, device="cuda")
+        got = host(a.decode_step(q, k, v, scale_for(D), rope=rope))
+        want = host(b.decode_step(q, k, v, scale_for(D), rope=rope))
+        np.testing.assert_array_equal(got, want)
+        if step % 6 == 5:
+            _check_mirror(a)
+    _check_mirror(a)
+    ka, va = a.read_buffers()
+    kb, vb = b.read_buffers()
+    np.testing.assert_array_equal(host(ka), host(kb))
+    np.testing.assert_array_equal(host(va), host(vb))

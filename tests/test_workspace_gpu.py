@@ -155,3 +155,65 @@ def test_bounded_wait_give_up_is_reported(gpu, prec):
     tol = 2e-2 if prec == sts_attn.PREC_BF16_MFMA else 1e-4
     assert np.abs(got - ref).max() < tol
 
+
+
+def test_capture_refused_prefill_leaves_cache_unchanged(gpu, fresh_stream):
+    """An f32 chunk prefill with split key ranges (32 x 128, 512 rows) on a fresh
+    stream needs workspace.  Inside a capture it is refused with STS_ERR_STATE
+    before anything is appended or the counters move: the state and both
+    buffers are those from before the call.  The same call then runs eagerly."""
+    H, D, M = 32, 128, 3000
+    s = fresh_stream
+    g = torch.Generator(device="cuda").manual_seed(13)
+    c = sts_attn.KVCache(M, H, D)
+    c.update(torch.randn((1, 256, H, D), generator=g, device="cuda"),
+             torch.randn((1, 256, H, D), generator=g, device="cuda"))
+    torch.cuda.synchronize()
+    before = c.state()
+    k0, v0 = c.read_buffers()
+    q, k, v = (torch.randn((512, H, D), generator=g, device="cuda") for _ in range(3))
+    out = torch.zeros((512, H, D), device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(sts_attn.StsError) as ei:
+            with torch.cuda.graph(graph, stream=s):
+                c.prefill(q, k, v, scale_for(D), sts_attn.PREC_F32, out=out, stream=s)
+        assert ei.value.code == sts_attn.STS_ERR_STATE
+    torch.cuda.synchronize()
+    after = c.state()
+    for f in ("offset", "len", "write_pos", "batch"):
+        assert getattr(after, f) == getattr(before, f), f
+    k1, v1 = c.read_buffers()
+    assert torch.equal(k1, k0) and torch.equal(v1, v0)
+    # Eagerly on the same stream: appended and attended as usual.
+    with torch.cuda.stream(s):
+        got = c.prefill(q, k, v, scale_for(D), sts_attn.PREC_F32, out=out, stream=s)
+    s.synchronize()
+    assert c.offset() == before.offset + 512 and c.seq_len() == 768
+    kc, vc = c.read_buffers()
+    st, ln = c.window()
+    ref = oracle.prefill_f64(host(q), host(kc)[0], host(vc)[0], st, ln, scale_for(D))
+    assert np.abs(host(got) - ref).max() < 1e-4
+
+
+def test_device_errors_refused_inside_capture(gpu, fresh_stream):
+    """Reading the device error word needs the stream drained and the swap run
+    now: inside a capture it is refused with STS_ERR_STATE (the capture stays
+    valid), and the word reads normally afterwards."""
+    s = fresh_stream
+    x = torch.zeros(16, device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            x.add_(1.0)
+            with pytest.raises(sts_attn.StsError) as ei:
+                sts_attn.device_errors(stream=s)
+            assert ei.value.code == sts_attn.STS_ERR_STATE
+            assert "captured" in str(ei.value)
+        graph.replay()
+        graph.replay()
+    s.synchronize()
+    assert torch.equal(x, torch.full((16,), 2.0, device="cuda"))
+    assert sts_attn.device_errors(stream=s) == 0

@@ -75,3 +75,51 @@ def test_noalloc_refuses_launches_beyond_the_array():
         sts_attn.STS_ERR_INVALID
     assert ctypes.c_int(fn(FAKE, FAKE, FAKE, FAKE + 4, FAKE, FAKE, 1, 32, 128, 3000, 0.1,
                            None)).value == sts_attn.STS_ERR_INVALID
+
+
+@pytest.mark.gpu
+def test_noalloc_replays_from_a_graph(gpu):
+    """The entry is for callers that cannot allocate, e.g. code under HIP graph
+    capture: a split decode (4 streams x 32 heads x 128 over 3000-row rings)
+    captured on a side stream replays bit-identically to an eager
+    sts_decode_ring, with eager calls of both entries between the replays."""
+    lib = sts_attn.load()
+    B, H, D, M = 4, 32, 128, 3000
+    g = torch.Generator(device="cuda").manual_seed(37)
+    kc = torch.randn((B, H, M, D), generator=g, device="cuda")
+    vc = torch.randn((B, H, M, D), generator=g, device="cuda")
+    q = torch.randn((B, H, D), generator=g, device="cuda")
+    lens = torch.tensor([M, 2000, 129, 1], dtype=torch.int32, device="cuda")
+    starts = torch.tensor([1234, 2999, 0, 7], dtype=torch.int32, device="cuda")
+    scale = scale_for(D)
+    want = torch.full((B, H, D), float("nan"), device="cuda")
+    got = torch.full((B, H, D), float("nan"), device="cuda")
+    side = torch.cuda.Stream()
+    sp = ctypes.c_void_p(side.cuda_stream)
+
+    def call(fn, out):
+        return fn(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), lens.data_ptr(),
+                  starts.data_ptr(), B, H, D, M, scale, sp)
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        assert call(lib.sts_decode_ring, want) == 0
+        assert call(lib.sts_decode_ring_noalloc, got) == 0  # the device's array is set up
+    side.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        assert call(lib.sts_decode_ring_noalloc, got) == 0
+    other = torch.full((B, H, D), float("nan"), device="cuda")
+    for rep in range(4):
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+        # Eager work on the shared array between replays (the counters it
+        # leaves at zero are the ones the graph's launch uses).
+        with torch.cuda.stream(side):
+            assert call(lib.sts_decode_ring_noalloc, other) == 0
+        side.synchronize()
+        np.testing.assert_array_equal(other.cpu().numpy(), want.cpu().numpy())
