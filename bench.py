@@ -35,6 +35,13 @@ FP32_PEAK_TFLOPS = 157.3       # fp32 MFMA
 LAYERS, H, D, M = 24, 32, 128, 3000
 CALIB_BYTES = 256 << 20
 
+# CPUs this process may run on (the CPU baseline pins one OpenMP thread to
+# each of the first `threads` of them while it is timed).
+try:
+    ALLOWED_CPUS = sorted(os.sched_getaffinity(0))
+except AttributeError:
+    ALLOWED_CPUS = list(range(os.cpu_count() or 1))
+
 
 def parse():
     ap = argparse.ArgumentParser()
@@ -73,6 +80,69 @@ class Timer:
         self.b.record(self.stream)
         self.torch.cuda.synchronize()
         self.ms = self.a.elapsed_time(self.b)
+
+
+PLAIN_READ_GRIDS = (256, 512, 1024, 2048)
+
+
+def time_plain_read(torch, sts, stream, pairs, workgroups, steps, warmup, graph=False):
+    """us per launch of sts_probe_stream_read over `pairs` ((a_ptr, a_bytes,
+    b_ptr, b_bytes), one launch each, in order), `workgroups` workgroups of
+    256 threads: a plain 16-byte nontemporal read of the same bytes a kernel
+    reads, the ceiling that kernel is compared with."""
+    lib = sts.load()
+    sink = torch.empty(max(PLAIN_READ_GRIDS), device="cuda")
+    sp = stream.cuda_stream
+
+    def run():
+        for a, na, b, nb in pairs:
+            rc = lib.sts_probe_stream_read(a, na, b, nb, workgroups, sink.data_ptr(), sp)
+            if rc:
+                raise RuntimeError(f"sts_probe_stream_read: {lib.sts_last_error().decode()}")
+    f = run
+    if graph:
+        run()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            run()
+        f = g.replay
+    for _ in range(warmup):
+        f()
+    with Timer(torch, stream) as t:
+        for _ in range(steps):
+            f()
+    return t.ms * 1e3 / (steps * len(pairs))
+
+
+def plain_read_block(torch, sts, stream, pairs, same_grid, kernel_us, steps, warmup,
+                     graph=False):
+    """The plain read of a kernel's bytes on the kernel's own grid and on the
+    fastest of PLAIN_READ_GRIDS, and the kernel's time as a fraction of each
+    (plain-read time / kernel time: 1.0 = the kernel runs at the plain-read rate)."""
+    grids = sorted(set(PLAIN_READ_GRIDS) | {same_grid})
+    t = {wg: time_plain_read(torch, sts, stream, pairs, wg, steps, warmup, graph) for wg in grids}
+    best = min(t, key=t.get)
+    nbytes = sum(na + nb for _, na, _, nb in pairs) / len(pairs)
+    return {"bytes_per_launch": int(nbytes),
+            "us_per_launch": round(t[same_grid], 3), "workgroups": same_grid,
+            "gbs": round(nbytes / (t[same_grid] * 1e-6) / 1e9, 1),
+            "best_us_per_launch": round(t[best], 3), "best_workgroups": best,
+            "best_gbs": round(nbytes / (t[best] * 1e-6) / 1e9, 1),
+            "by_workgroups_us": {str(k): round(v, 3) for k, v in t.items()},
+            "kernel_us_per_launch": round(kernel_us, 3),
+            "kernel_frac_of_plain_read": round(t[same_grid] / kernel_us, 4),
+            "kernel_frac_of_best_plain_read": round(t[best] / kernel_us, 4)}
+
+
+def decode_grid(torch):
+    """Workgroups of one config-2 decode launch: splits per head x heads, the
+    splits chosen as the launcher does (about one workgroup per CU, chunks of
+    whole 64-row units)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    want = max(1, -(-cus // H))
+    chunk = -(-(-(-M // want)) // 64) * 64
+    chunk = min(max(chunk, 64), 512 // 64 * 64)
+    return -(-M // chunk) * H
 
 
 def bench_decode(torch, sts, stream, steps, warmup):
@@ -123,7 +193,16 @@ def bench_decode(torch, sts, stream, steps, warmup):
     us_frame = t.ms * 1e3 / steps
     us_launch = us_frame / LAYERS
     us_attend = ta.ms * 1e3 / steps / LAYERS
+    # The same K/V bytes of the same 24 caches read plainly, launch by launch.
+    kv_bytes = H * M * D * 4
+    pairs = []
+    for c in caches:
+        kp, vp, _ = c.ensure_allocated(1)
+        pairs.append((kp, kv_bytes, vp, kv_bytes))
+    plain = plain_read_block(torch, sts, stream, pairs, decode_grid(torch), us_launch, steps,
+                             min(warmup, 5))
     return {
+        "plain_read": plain,
         "us_per_frame": us_frame,
         "us_per_launch": us_launch,
         "bytes_per_launch": bytes_layer,
@@ -317,6 +396,32 @@ def bench_q4k(torch, sts, stream, steps, warmup):
            "gbs": (w_bytes + io_bytes) / (us * 1e-6) / 1e9}
     res["frac"] = res["gbs"] / HBM_PEAK_GBS
     res["_layers"] = layers
+    # Per-launch figures of each projection alone (graph of its 24 launches),
+    # beside a plain read of the same weight bytes (the kernels' grid is 512
+    # workgroups of 256 threads at these shapes).
+    for name, idx, n in (("in_proj", 0, 3 * K), ("out_proj", 1, K)):
+        ws = [lw[idx] for lw in layers]
+        yo = qkv if idx == 0 else y
+
+        def proj():
+            for w in ws:
+                sts.q4k_matmul(x, w, residual=None if idx == 0 else x, out=yo, stream=stream)
+        proj()
+        gp = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gp, stream=stream):
+            proj()
+        for _ in range(warmup):
+            gp.replay()
+        with Timer(torch, stream) as tp:
+            for _ in range(steps):
+                gp.replay()
+        us_l = tp.ms * 1e3 / (steps * LAYERS)
+        nbytes = n * K // 256 * 144
+        res[name + "_us_per_launch"] = us_l
+        res[name + "_plain_read"] = plain_read_block(
+            torch, sts, stream, [(w.raw.data_ptr(), nbytes, 0, 0) for w in ws], 512, us_l, steps,
+            min(warmup, 5), graph=True)
+        del gp
     for name, (n, k) in (("linear_in", (22528, K)), ("linear_out", (K, 11264))):
         ws = [sts.Q4KTensor(q4k_random(torch, g, n, k), (n, k)) for _ in range(4)]
         xi = torch.randn((1, 1, k), generator=g, device="cuda")
@@ -446,23 +551,50 @@ def cpu_info():
     except OSError:
         pass
     nproc = os.cpu_count() or 1
-    try:
-        allowed = len(os.sched_getaffinity(0))
-    except AttributeError:
-        allowed = nproc
+    allowed = len(ALLOWED_CPUS)
     env = os.environ.get("OMP_NUM_THREADS", "")
     threads = min(allowed, int(env)) if env.isdigit() and int(env) > 0 else allowed
     return {"cpu_model": model, "nproc": nproc, "affinity": allowed, "threads": threads,
-            "omp_num_threads_env": env or None}
+            "omp_num_threads_env": env or None,
+            "pinned_cpus": ALLOWED_CPUS[:threads]}
 
 
-def _median_time(fn, reps):
+def _times_us(fn, reps):
+    """Wall time of `reps` calls of fn (after the caller's warm-up): min,
+    median and max in microseconds."""
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
         fn()
-        ts.append(time.perf_counter() - t0)
-    return float(sorted(ts)[len(ts) // 2])
+        ts.append((time.perf_counter() - t0) * 1e6)
+    ts.sort()
+    return {"min_us": ts[0], "median_us": ts[len(ts) // 2], "max_us": ts[-1], "reps": reps}
+
+
+class _Pinned:
+    """OpenMP thread t of the oracle's `threads`-thread regions runs on
+    ALLOWED_CPUS[t] inside the block; afterwards the threads may run anywhere
+    again."""
+
+    def __init__(self, oracle, threads):
+        self.oracle, self.cpus = oracle, ALLOWED_CPUS[:threads]
+
+    def __enter__(self):
+        self.failed = self.oracle.bind_threads(self.cpus, True)
+        return self
+
+    def __exit__(self, *exc):
+        self.oracle.bind_threads(ALLOWED_CPUS, False)
+        self.oracle.set_num_threads(len(self.cpus))
+
+
+def _baseline(all_threads, one_thread, info, sample, one_thread_scale=1):
+    """The cpu_baseline block: `value` is the median on all allowed threads;
+    the spread and the one-thread figures ride along."""
+    one = {k: (v * one_thread_scale if k.endswith("_us") else v) for k, v in one_thread.items()}
+    return {"value": all_threads["median_us"], "unit": "us/frame", "cores": info["threads"],
+            "kind": "port", **all_threads, "one_thread_us": one["median_us"],
+            "one_thread": one, **info, "sample": sample}
 
 
 def cpu_baseline_depformer_frame(torch, cfg, w, args):
@@ -483,17 +615,15 @@ def cpu_baseline_depformer_frame(torch, cfg, w, args):
     def stream(b):
         oracle.depformer_generate(ow, th[b], int(text[b]), top_k, temp, pen, rand[b], pt[b],
                                   npn[b])
-    oracle.set_num_threads(info["threads"])
-    stream(0)
-    us = _median_time(lambda: [stream(b) for b in range(DEPF_STREAMS)], 1) * 1e6
-    oracle.set_num_threads(1)
-    us1 = _median_time(lambda: stream(0), 1) * 1e6 * DEPF_STREAMS
-    oracle.set_num_threads(info["threads"])
-    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
-            "one_thread_us": us1, **info,
-            "sample": f"all {DEPF_STREAMS} streams of the benchmarked frame, one after another "
-                      f"(OpenMP inside each op); the 1-thread figure runs stream 0 and scales "
-                      f"x{DEPF_STREAMS}"}
+    with _Pinned(oracle, info["threads"]):
+        stream(0)
+        allt = _times_us(lambda: [stream(b) for b in range(DEPF_STREAMS)], 5)
+    with _Pinned(oracle, 1):
+        one = _times_us(lambda: stream(0), 5)
+    return _baseline(allt, one, info,
+                     f"all {DEPF_STREAMS} streams of the benchmarked frame, one after another "
+                     f"(OpenMP inside each op), 5 repetitions; the 1-thread figures run stream 0 "
+                     f"and scale x{DEPF_STREAMS}", one_thread_scale=DEPF_STREAMS)
 
 
 def cpu_baseline_q4k(torch, layers):
@@ -511,16 +641,15 @@ def cpu_baseline_q4k(torch, layers):
         for wi, wo in ws:
             oracle.q4k_matvec_wgsl(wi, x, 3 * 4096)
             oracle.q4k_matvec_wgsl(wo, x, 4096)
-    oracle.set_num_threads(info["threads"])
-    frame()
-    us = _median_time(frame, 3) * 1e6
-    oracle.set_num_threads(1)
-    us1 = _median_time(frame, 1) * 1e6
-    oracle.set_num_threads(info["threads"])
-    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
-            "one_thread_us": us1, **info,
-            "sample": f"the whole frame: in_proj + out_proj of all {LAYERS} layers (x0 of one "
-                      f"frame), oracle shader-order f32 Q4_K matvec"}
+    with _Pinned(oracle, info["threads"]):
+        frame()
+        allt = _times_us(frame, 7)
+    with _Pinned(oracle, 1):
+        one = _times_us(frame, 5)
+    return _baseline(allt, one, info,
+                     f"the whole frame: in_proj + out_proj of all {LAYERS} layers (x0 of one "
+                     f"frame), oracle shader-order f32 Q4_K matvec; 7 repetitions on all "
+                     f"threads, 5 on one")
 
 
 def cpu_baseline(torch, dec):
@@ -547,17 +676,16 @@ def cpu_baseline(torch, dec):
 
     def frame():
         oracle.decode_frame_wgsl(qs, kcs, vcs, starts, lens, scale)
-    oracle.set_num_threads(info["threads"])
-    frame()
-    us = _median_time(frame, 5) * 1e6
-    oracle.set_num_threads(1)
-    us1 = _median_time(frame, 3) * 1e6
-    oracle.set_num_threads(info["threads"])
-    return {"value": us, "unit": "us/frame", "cores": info["threads"], "kind": "port",
-            "one_thread_us": us1, **info,
-            "sample": f"the whole frame: {LAYERS} layers x {H} heads x {M} rows (the benchmarked "
-                      f"caches and queries, attention only), oracle shader-order f32 attention, "
-                      f"OpenMP over (layer, head)"}
+    with _Pinned(oracle, info["threads"]):
+        frame()
+        frame()
+        allt = _times_us(frame, 9)
+    with _Pinned(oracle, 1):
+        one = _times_us(frame, 5)
+    return _baseline(allt, one, info,
+                     f"the whole frame: {LAYERS} layers x {H} heads x {M} rows (the benchmarked "
+                     f"caches and queries, attention only), oracle shader-order f32 attention, "
+                     f"OpenMP over (layer, head); 9 repetitions on all threads, 5 on one")
 
 
 def load_traffic():
@@ -644,7 +772,11 @@ def main():
                      "traffic": load_traffic(),
                      "kernel": "decode_kernel<128,4>",
                      "bytes_per_launch": dec["bytes_per_launch"],
-                     "us_per_launch": round(dec["us_per_launch"], 3)},
+                     "us_per_launch": round(dec["us_per_launch"], 3),
+                     # A plain read of the same K/V bytes, same grid, same caches.
+                     "plain_read_us_per_launch": dec["plain_read"]["us_per_launch"],
+                     "kernel_frac_of_plain_read": dec["plain_read"]["kernel_frac_of_plain_read"]},
+        "plain_read": dec["plain_read"],
         "cpu_baseline": cpu,
         "decode_attend_only": {"us_per_launch": round(dec["attend_only_us_per_launch"], 3),
                                "gbs": round(dec["attend_only_gbs"], 1)},

@@ -551,6 +551,22 @@ int sts_depformer_generate(sts_depformer* d, const float* temporal_hidden,
                            const uint32_t* penalty_tokens, const uint32_t* num_penalty,
                            uint32_t* tokens, float* logits, void* stream);
 
+/* ---------------------------------------------------------------------- */
+/* Measurement                                                              */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * Plain-read roofline probe: no counterpart in the reference.  Reads a_bytes
+ * at a and b_bytes at b (multiples of 16, 16-byte aligned; b may be null
+ * with b_bytes 0) once, with 16-byte nontemporal loads and nothing else,
+ * `workgroups` workgroups of 256 threads each streaming a contiguous share of
+ * both buffers; stores one float per workgroup to sink[0..workgroups).
+ * Timed on a kernel's own bytes and grid, it measures what a read of those
+ * bytes reaches on the device, the ceiling that kernel is compared with.
+ */
+int sts_probe_stream_read(const void* a, uint64_t a_bytes, const void* b, uint64_t b_bytes,
+                          uint32_t workgroups, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

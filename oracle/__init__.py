@@ -98,6 +98,7 @@ def _load():
                                           ctypes.POINTER(_u32), _f32p, _f32p]),
         "orc_num_threads": (ctypes.c_int, []),
         "orc_set_num_threads": (None, [ctypes.c_int]),
+        "orc_bind_threads": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -306,6 +307,13 @@ def num_threads() -> int:
 
 def set_num_threads(n: int) -> None:
     lib().orc_set_num_threads(n)
+
+
+def bind_threads(cpus, pin: bool = True) -> int:
+    """Runs OpenMP thread t of the following len(cpus)-thread regions on cpus[t]
+    (pin) or on any of cpus (unpin); returns how many bindings failed."""
+    arr = (ctypes.c_int * len(cpus))(*cpus)
+    return lib().orc_bind_threads(arr, len(cpus), 1 if pin else 0)
 
 
 # ---- Q4_K -------------------------------------------------------------------

@@ -9,9 +9,12 @@
  * Reference paths are relative to crates/sts-wasm/src/ of
  * idle-intelligence/sts-web.
  */
+#define _GNU_SOURCE
 #include "oracle.h"
 
 #include <float.h>
+#include <pthread.h>
+#include <sched.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -876,4 +879,34 @@ void orc_set_num_threads(int n) {
 #else
   (void)n;
 #endif
+}
+
+/* Timing support for the CPU baseline: OpenMP thread t of the next n-thread
+ * teams runs on CPU cpus[t] only (pin = 1), or on any of cpus[0..n) again
+ * (pin = 0).  libgomp keeps its team threads between parallel regions, so the
+ * binding holds for the regions that follow.  Returns the number of threads
+ * whose binding failed. */
+int orc_bind_threads(const int* cpus, int n, int pin) {
+  int failed = 0;
+#if defined(_OPENMP) && defined(__linux__)
+  if (n <= 0) return 0;
+  omp_set_num_threads(n);
+#pragma omp parallel reduction(+ : failed)
+  {
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    const int t = omp_get_thread_num();
+    if (pin) {
+      CPU_SET(cpus[t % n], &set);
+    } else {
+      for (int i = 0; i < n; ++i) CPU_SET(cpus[i], &set);
+    }
+    failed += pthread_setaffinity_np(pthread_self(), sizeof set, &set) != 0;
+  }
+#else
+  (void)cpus;
+  (void)n;
+  (void)pin;
+#endif
+  return failed;
 }

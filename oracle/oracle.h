@@ -234,6 +234,7 @@ void orc_depformer_generate(const orc_depformer_cfg* cfg, const orc_depformer_we
 /* Number of OpenMP threads the oracle uses (for the CPU-baseline record). */
 int orc_num_threads(void);
 void orc_set_num_threads(int n);
+int orc_bind_threads(const int* cpus, int n, int pin);
 
 #ifdef __cplusplus
 }

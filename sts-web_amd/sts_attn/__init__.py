@@ -108,6 +108,7 @@ SIGNATURES = {
     "sts_depformer_destroy": (_int, [_vp]),
     "sts_depformer_generate": (_int, [_vp, _vp, _vp, _u32, _u32, _f32, _f32, _vp, _vp, _vp, _vp,
                                       _vp, _vp]),
+    "sts_probe_stream_read": (_int, [_vp, _u64, _vp, _u64, _u32, _vp, _vp]),
 }
 
 _lib = None
@@ -511,6 +512,16 @@ def take_device_errors(stream=None) -> int:
 def set_wait_limit(polls: int) -> None:
     """Test hook: polls after which the kernels' bounded waits give up (0 = default)."""
     _check(load().sts_debug_set_wait_limit(polls))
+
+
+def probe_stream_read(a: torch.Tensor, b: Optional[torch.Tensor], workgroups: int,
+                      sink: torch.Tensor, stream=None) -> None:
+    """Plain-read roofline probe: reads a and b once (16-byte nontemporal
+    loads, `workgroups` workgroups of 256 threads); one float per workgroup
+    goes to sink."""
+    _check(load().sts_probe_stream_read(_ptr(a), a.numel() * a.element_size(), _ptr(b),
+                                        0 if b is None else b.numel() * b.element_size(),
+                                        workgroups, _ptr(sink), _stream(stream)))
 
 
 def softmax_scale(head_dim: int) -> float:
