@@ -91,6 +91,8 @@ def _load():
         "orc_embed_q4_0": (None, [ctypes.c_void_p, _u32, _u32, _u32, _f32p]),
         "orc_sample_topk_wgsl": (_u32, [_f32p, _u32, _u32, ctypes.c_float, ctypes.c_float,
                                         ctypes.c_float, ctypes.POINTER(_u32), _u32]),
+        "orc_sample_topk_wgsl_ex": (_u32, [_f32p, _u32, _u32, ctypes.c_float, ctypes.c_float,
+                                        ctypes.c_float, ctypes.POINTER(_u32), _u32, ctypes.POINTER(_u32), _f32p]),
         "orc_depformer_generate": (None, [ctypes.POINTER(DepformerCfg),
                                           ctypes.POINTER(DepformerWeightPtrs), _f32p, _u32,
                                           _u32, ctypes.c_float, ctypes.c_float, _f32p,
@@ -440,6 +442,20 @@ def sample_topk_wgsl(logits, top_k, temperature, penalty, rand, penalty_tokens=(
                                      float(penalty), float(rand),
                                      pt.ctypes.data_as(ctypes.POINTER(_u32)), pt.size)
     return int(tok), lg
+
+
+def sample_topk_wgsl_detail(logits, top_k, temperature, penalty, rand, penalty_tokens=()):
+    """shader_sample_topk.wgsl on one row (top_k > 1); returns (token, the
+    logit indices of the sorted slots, the draw's running totals)."""
+    lg = np.array(logits, dtype=np.float32, copy=True)
+    pt = np.ascontiguousarray(np.asarray(penalty_tokens, dtype=np.uint32).reshape(-1))
+    idx = np.zeros(top_k, np.uint32)
+    cum = np.zeros(top_k, np.float32)
+    tok = lib().orc_sample_topk_wgsl_ex(_p32(lg), lg.size, int(top_k), float(temperature),
+                                        float(penalty), float(rand),
+                                        pt.ctypes.data_as(ctypes.POINTER(_u32)), pt.size,
+                                        idx.ctypes.data_as(ctypes.POINTER(_u32)), _p32(cum))
+    return int(tok), idx, cum
 
 
 def q4_0_random_table(seed, vocab, dim, scale_lo=0x2000, scale_hi=0x2C00):

@@ -700,6 +700,15 @@ void orc_embed_q4_0(const uint8_t* table, uint32_t vocab, uint32_t dim, uint32_t
 uint32_t orc_sample_topk_wgsl(float* logits, uint32_t V, uint32_t top_k, float temperature,
                               float penalty, float rand, const uint32_t* penalty_tokens,
                               uint32_t num_penalty) {
+  return orc_sample_topk_wgsl_ex(logits, V, top_k, temperature, penalty, rand, penalty_tokens,
+                                 num_penalty, NULL, NULL);
+}
+
+/* As orc_sample_topk_wgsl; for top_k > 1 also stores the sorted slots' logit
+ * indices and the running totals of the draw (top_k each) when given. */
+uint32_t orc_sample_topk_wgsl_ex(float* logits, uint32_t V, uint32_t top_k, float temperature,
+                                 float penalty, float rand, const uint32_t* penalty_tokens,
+                                 uint32_t num_penalty, uint32_t* idx_out, float* cum_out) {
   /* Repetition penalty, shader_sample_topk.wgsl:56-69. */
   for (uint32_t p = 0; p < num_penalty; ++p) {
     const uint32_t tok = penalty_tokens[p];
@@ -779,22 +788,30 @@ uint32_t orc_sample_topk_wgsl(float* logits, uint32_t V, uint32_t top_k, float t
     vals[sj + 1] = kv;
     idxs[sj + 1] = ki;
   }
-  /* Softmax over the K and the cumulative draw, :198-221. */
+  /* Softmax over the K and the cumulative draw, :198-221.  WGSL's exp has an
+   * implementation-defined error bound (several ulp), so the reference fixes no
+   * particular rounding of it; exp(v - max) is taken here correctly rounded to
+   * f32 (exp in f64, then rounded), which the GPU sampler computes the same
+   * way, so the draw is reproducible bit for bit. */
   float max_v = vals[0];
   for (uint32_t j = 1; j < K; ++j)
     if (vals[j] > max_v) max_v = vals[j];
   float sum = 0.f;
   for (uint32_t j = 0; j < K; ++j) {
-    vals[j] = expf(vals[j] - max_v);
+    vals[j] = (float)exp((double)(vals[j] - max_v));
     sum = sum + vals[j];
   }
   float cum = 0.f;
   uint32_t tok = idxs[K - 1];
+  int found = 0;
   for (uint32_t j = 0; j < K; ++j) {
     cum = cum + vals[j] / sum;
-    if (rand < cum) {
+    if (cum_out) cum_out[j] = cum;
+    if (idx_out) idx_out[j] = idxs[j];
+    if (!found && rand < cum) {
       tok = idxs[j];
-      break;
+      found = 1;
+      if (!cum_out && !idx_out) break;
     }
   }
   free(vals);

@@ -190,6 +190,9 @@ void orc_embed_q4_0(const uint8_t* table, uint32_t vocab, uint32_t dim, uint32_t
 uint32_t orc_sample_topk_wgsl(float* logits, uint32_t V, uint32_t top_k, float temperature,
                               float penalty, float rand, const uint32_t* penalty_tokens,
                               uint32_t num_penalty);
+uint32_t orc_sample_topk_wgsl_ex(float* logits, uint32_t V, uint32_t top_k, float temperature,
+                                 float penalty, float rand, const uint32_t* penalty_tokens,
+                                 uint32_t num_penalty, uint32_t* idx_out, float* cum_out);
 
 typedef struct orc_depformer_cfg {
   uint32_t num_steps, num_layers, dim, num_heads, ffn, temporal_dim;

@@ -352,14 +352,25 @@ __device__ __forceinline__ uint32_t count_above(const uint64_t* L, uint64_t x) {
   return pos + ((STRICT ? y > x : y >= x) ? 1u : 0u);
 }
 
-// shader_sample_topk.wgsl for one stream per workgroup.  Penalty, temperature
-// and (top_k <= 1) the argmax follow the shader's lanes and tree exactly.  The
-// top K are found by a radix select of the K-th largest value and ranked by
-// (value descending, index ascending) keys, per-wave bitonic sorts merged by
-// binary-search ranks, which for distinct values is the shader's selection
-// and insertion sort; the softmax values are the shader's (exp of v - max),
-// their sum and running total come from a wave scan.  Thread t holds logits t, t + 256, ... in registers: NJ
-// of them, NJ * 256 >= V.
+// shader_sample_topk.wgsl for one stream per workgroup, token for token.
+// Penalty, temperature and (top_k <= 1) the argmax follow the shader's lanes
+// and tree exactly.  The top K are found by a radix select of the K-th
+// largest value and ranked by (value descending, index ascending) keys,
+// per-wave bitonic sorts merged by binary-search ranks, which is the shader's
+// selection and insertion sort unless logits the order depends on are equal;
+// then wave 0 replays the shader's selection (first minimum replaced) and the
+// slots are ranked as its stable sort ranks them.  exp(v - max) is taken
+// correctly rounded; the draw comes from a wave scan, checked against the
+// shader's running total and redone on one lane where they could differ.
+// Thread t holds logits t, t + 256, ... in registers: NJ of them,
+// NJ * 256 >= V.
+
+// Bound on how far the sampler's wave-scan running total can be from the
+// shader's single-lane one: each is within about 2K ulps of 1 of the exact
+// total (positive terms, K <= 256: 2 * 256 * 2^-24 = 3.1e-5), so they differ
+// by less than 6.2e-5 < 2^-13.
+constexpr float kDrawSlack = 1.0f / 8192.0f;
+
 template <int NJ>
 __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) {
   __shared__ float vals[NJ * 256];
@@ -372,6 +383,9 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   __shared__ float s_maxv;
   __shared__ uint32_t s_ptok[kMaxPenalty];
   __shared__ uint64_t sbuf[2 * kMaxTopK];
+  __shared__ uint32_t slot_idx[kMaxTopK];  // replayed selection: slot -> logit index
+  __shared__ uint32_t s_tie[2];            // keys >= the K-th, any equal neighbours
+  __shared__ float cumv[kMaxTopK];         // running totals (or weights) of the draw
   static_assert(kMaxTopK == 256, "one key per thread in the ranking sort");
   const uint32_t tid = threadIdx.x, b = blockIdx.x, V = p.V;
   const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -549,40 +563,138 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   if (tid >= Ks) ck[tid] = 0;
   __syncthreads();
 
-  // Rank: value descending, index ascending.  Each wave sorts its 64 keys;
-  // a key's rank is its place in its wave's list plus the keys above it in
-  // the other three lists (equal keys, the padding zeros, count as above
-  // when they are in a lower wave, so the ranks are distinct).
-  uint64_t key = ck[tid];
-  wave_bitonic_sort<2>(key, lane);
-  uint64_t* lists = sbuf;  // each thread overwrites only the slot it read
-  lists[tid] = key;
-  __syncthreads();
-  uint32_t rank = lane;
+  // Rank the keys of ck, descending.  Each wave sorts its 64 keys; a key's
+  // rank is its place in its wave's list plus the keys above it in the other
+  // three lists (equal keys, the padding zeros, count as above when they are
+  // in a lower wave, so the ranks are distinct).  Leaves the key of rank tid
+  // in sbuf[256 + tid] and returns it.
+  auto rank_keys = [&]() -> uint64_t {
+    uint64_t key = ck[tid];
+    wave_bitonic_sort<2>(key, lane);
+    uint64_t* lists = sbuf;  // each thread overwrites only the slot it read
+    lists[tid] = key;
+    __syncthreads();
+    uint32_t rank = lane;
 #pragma unroll
-  for (uint32_t i = 1; i < 4; ++i) {
-    const uint32_t w2 = (wave + i) & 3u;
-    rank += w2 > wave ? count_above<true>(lists + 64 * w2, key)
-                      : count_above<false>(lists + 64 * w2, key);
+    for (uint32_t i = 1; i < 4; ++i) {
+      const uint32_t w2 = (wave + i) & 3u;
+      rank += w2 > wave ? count_above<true>(lists + 64 * w2, key)
+                        : count_above<false>(lists + 64 * w2, key);
+    }
+    sbuf[256 + rank] = key;
+    __syncthreads();
+    return sbuf[256 + tid];
+  };
+  // Value descending, index ascending: the shader's selection and insertion
+  // sort (:134-196) whenever no two of the logits the order depends on are
+  // equal.
+  uint64_t key = rank_keys();
+  bool emulated = false;
+  if (V > K) {
+    // Ties: two of the K taken with equal values (the stable insertion sort
+    // orders them by the shader's slot, not by index), or a logit left out
+    // with the value of the K-th (which of those the shader keeps depends on
+    // its slots).  Then wave 0 replays the shader's selection itself.
+    const uint32_t tkey = (uint32_t)(sbuf[256 + K - 1] >> 32);
+    bool tie = tid + 1 < K && (uint32_t)(sbuf[256 + tid + 1] >> 32) == (uint32_t)(key >> 32);
+    uint32_t n_ge = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) n_ge += (tid + 256u * j < V && k[j] >= tkey) ? 1u : 0u;
+    if (tid == 0) s_tie[0] = s_tie[1] = 0;
+    __syncthreads();
+    if (n_ge) atomicAdd(&s_tie[0], n_ge);
+    if (tie) s_tie[1] = 1;
+    __syncthreads();
+    emulated = s_tie[1] != 0 || s_tie[0] > K;
   }
-  sbuf[256 + rank] = key;
-  __syncthreads();
-  key = sbuf[256 + tid];
+  if (emulated) {
+    // The logits' keys in index order (vals is free once the keys exist).
+    uint32_t* lk = reinterpret_cast<uint32_t*>(vals);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (tid + 256u * j < V) lk[tid + 256u * j] = k[j];
+    if (tid >= K) ck[tid] = 0;
+    __syncthreads();
+    if (wave == 0) {
+      // Slot s = lane + 64c holds (key << 32 | s) and its logit's index.
+      // Thread 0's loop (:148-178): slots 0..K-1 start with logits 0..K-1;
+      // logit j >= K replaces the first slot holding the minimum when it is
+      // strictly greater, and the minimum is found again.
+      uint64_t sk[4];
+      uint32_t sidx[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t sl = lane + 64u * c;
+        sk[c] = sl < K ? ((uint64_t)lk[sl] << 32) | sl : ~0ull;
+        sidx[c] = sl;
+      }
+      auto wave_min = [&]() {
+        uint64_t m = sk[0];
+#pragma unroll
+        for (int c = 1; c < 4; ++c) m = sk[c] < m ? sk[c] : m;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)m, off, 64);
+          const uint32_t hi = __shfl_xor((uint32_t)(m >> 32), off, 64);
+          const uint64_t o = ((uint64_t)hi << 32) | lo;
+          m = o < m ? o : m;
+        }
+        return m;
+      };
+      uint64_t mn = wave_min();
+      for (uint32_t j0 = K; j0 < V; j0 += 64) {
+        const uint32_t j = j0 + lane;
+        const bool in = j < V;
+        const uint32_t kj = in ? lk[j] : 0u;
+        uint64_t bits = __ballot(in && kj > (uint32_t)(mn >> 32));
+        while (bits) {
+          const int bl = __builtin_ctzll(bits);
+          const uint32_t kb = __builtin_amdgcn_readlane(kj, bl);
+          const uint32_t sl = (uint32_t)mn;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (lane + 64u * c == sl) {
+              sk[c] = ((uint64_t)kb << 32) | sl;
+              sidx[c] = j0 + (uint32_t)bl;
+            }
+          mn = wave_min();
+          bits &= ~((2ull << bl) - 1ull);
+          bits &= __ballot(in && kj > (uint32_t)(mn >> 32));
+        }
+      }
+      // Ranked as the insertion sort orders them: value descending, slot
+      // ascending among equal values.
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t sl = lane + 64u * c;
+        if (sl < K) {
+          ck[sl] = (sk[c] & 0xFFFFFFFF00000000ull) | (0xFFFFFFFFu - sl);
+          slot_idx[sl] = sidx[c];
+        }
+      }
+    }
+    __syncthreads();
+    key = rank_keys();
+  }
   // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
   const bool real = tid < Ks;
   const float v = real ? key_value((uint32_t)(key >> 32)) : -3.402823466e+38f;
-  ri[tid] = real ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+  const uint32_t low = 0xFFFFFFFFu - (uint32_t)key;
+  ri[tid] = real ? (emulated ? slot_idx[low] : low) : 0u;
   if (tid == 0) s_maxv = v;
   __syncthreads();
-  // Softmax over the K (:198-210) and the cumulative draw (:212-221).
+  // Softmax over the K (:198-210): exp(v - max) correctly rounded to f32
+  // (through f64), the rounding the oracle takes for WGSL's exp.
   const float max_v = s_maxv;
-  if (tid < K) ev[tid] = expf(v - max_v);
+  if (tid < K) ev[tid] = (float)exp((double)(v - max_v));
   __syncthreads();
   if (tid < 64) {
-    // Wave 0: lane l holds values 4l..4l+3.  The sum and the running total
-    // are formed by a wave scan rather than the shader's single-lane loop, a
-    // different f32 order: the draw can differ only where rand lies within
-    // rounding of a cumulative boundary.
+    // The cumulative draw (:212-221).  Wave 0: lane l holds values 4l..4l+3;
+    // the sum and the running total come from a wave scan, a different f32
+    // order from the shader's single-lane loop, less than kDrawSlack away
+    // from it.  The scan's pick is therefore the shader's whenever rand lies
+    // further than kDrawSlack from the boundaries around it; otherwise lane 0
+    // redoes the shader's loop.
     float e[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) e[c] = 4 * tid + c < K ? ev[4 * tid + c] : 0.f;
@@ -603,6 +715,9 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
       if (tid >= off) pre += w;
     }
     pre -= run;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (4 * tid + c < K) cumv[4 * tid + c] = pre + q[c];
     const float rnd = p.rand[(size_t)b * p.rs_stride];
     int first = 4;
 #pragma unroll
@@ -613,6 +728,44 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
     if (hits) {
       const int lane0 = __builtin_ctzll(hits);
       pick = 4 * lane0 + __shfl(first, lane0, 64);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Certain when rand sits clear of the pick's upper boundary (or, with no
+    // hit, of the last total) and of its lower one.
+    const bool sure = hits ? (rnd < cumv[pick] - kDrawSlack &&
+                              (pick == 0 || rnd >= cumv[pick - 1] + kDrawSlack))
+                           : rnd >= cumv[K - 1] + kDrawSlack;
+    if (!sure) {
+      // The shader's order: sum in slot order on one lane, each weight
+      // divided by it, the running total in slot order.
+      if (tid == 0) {
+        float sq = 0.f;
+        for (uint32_t j = 0; j < K; ++j) sq = sq + ev[j];
+        s_maxv = sq;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float sq = s_maxv;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (4 * tid + c < K) cumv[4 * tid + c] = e[c] / sq;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (tid == 0) {
+        float cum = 0.f;
+        pick = K - 1;
+        for (uint32_t j = 0; j < K; ++j) {
+          cum = cum + cumv[j];
+          if (rnd < cum) {
+            pick = j;
+            break;
+          }
+        }
+      }
     }
     if (tid == 0) *outp = ri[pick];
   }

@@ -17,7 +17,7 @@ import torch
 
 import oracle
 import sts_attn
-from test_oracle_depformer import CFG, _sample_np
+from test_oracle_depformer import CFG
 
 pytestmark = pytest.mark.gpu
 
@@ -154,35 +154,9 @@ def test_sample_topk_against_oracle(gpu, V, K):
     npn = rng.integers(0, 31, size=B).astype(np.uint32)
     got = host(sts_attn.sample_top_k(dev(logits), K, 0.8, 1.3, dev(rand), dev(pt.view(np.int32)),
                                      dev(npn.view(np.int32)))).view(np.uint32)
-    checked = 0
     for b in range(B):
         want, _ = oracle.sample_topk_wgsl(logits[b], K, 0.8, 1.3, float(rand[b]), pt[b, :npn[b]])
-        _, safe = _sample_np(logits[b], K, 0.8, 1.3, float(rand[b]), pt[b, :npn[b]])
-        if safe:
-            assert got[b] == want, (b, got[b], want)
-            checked += 1
-    assert checked >= B - 2
-
-
-def _sample_ties(logits, top_k, temp, penalty, rand, ptoks):
-    """The kernel's rule where values repeat: the top k by value descending,
-    ties by index ascending (so the k-th largest value's ties go to the lowest
-    indices), then the cumulative draw.  Returns (token, safe): safe is False
-    when rand lies within 1e-5 of a cumulative boundary."""
-    lg = np.array(logits, np.float32)
-    for t in dict.fromkeys(int(t) for t in ptoks):
-        if t < lg.size:
-            lg[t] = lg[t] / np.float32(penalty) if lg[t] > 0 else lg[t] * np.float32(penalty)
-    lg = lg / np.float32(temp)
-    srt = np.argsort(-lg.astype(np.float64), kind="stable")
-    k = min(top_k, lg.size)
-    v = np.full(top_k, -3.402823466e+38)
-    v[:k] = lg[srt[:k]]
-    p = np.exp(v - v[0])
-    cum = np.cumsum(p / p.sum())
-    j = min(int(np.searchsorted(cum, rand, side="right")), top_k - 1)
-    tok = int(srt[j]) if j < k else 0
-    return tok, bool(np.min(np.abs(cum - rand)) > 1e-5)
+        assert got[b] == want, (b, got[b], want)
 
 
 @pytest.mark.parametrize("V,K", [(2048, 250), (2048, 256), (2048, 20), (2048, 1), (300, 2),
@@ -191,9 +165,10 @@ def _sample_ties(logits, top_k, temp, penalty, rand, ptoks):
 def test_sample_topk_ties(gpu, V, K):
     """Logits on a coarse grid, so values repeat and the k-th largest is
     tied: rows with every value equal, rows with two values, a row of -0 and
-    +0 (equal as floats), rows on a 0.25 grid.  top_k > 1 follows the ranking rule above; top_k = 1 the shader's
-    lane and tree argmax (the oracle), whose choice among equal maxima is
-    not the lowest index."""
+    +0 (equal as floats), rows on a 0.25 grid.  Every token equals the
+    oracle's (the shader's selection by replacing the first minimum, its
+    stable insertion sort and its running total; top_k = 1 its lane and tree
+    argmax)."""
     B = 24
     rng = np.random.default_rng(V * 13 + K)
     logits = (np.round(rng.standard_normal((B, V)) * 4) / 4).astype(np.float32)
@@ -213,18 +188,45 @@ def test_sample_topk_ties(gpu, V, K):
     npn[:6] = 0
     got = host(sts_attn.sample_top_k(dev(logits), K, 0.8, 1.3, dev(rand), dev(pt.view(np.int32)),
                                      dev(npn.view(np.int32)))).view(np.uint32)
-    checked = 0
     for b in range(B):
-        if K <= 1:
-            want, _ = oracle.sample_topk_wgsl(logits[b], K, 0.8, 1.3, float(rand[b]),
-                                              pt[b, :npn[b]])
-            safe = True
-        else:
-            want, safe = _sample_ties(logits[b], K, 0.8, 1.3, float(rand[b]), pt[b, :npn[b]])
-        if safe:
-            assert got[b] == want, (b, got[b], want)
-            checked += 1
-    assert checked >= B - 3
+        want, _ = oracle.sample_topk_wgsl(logits[b], K, 0.8, 1.3, float(rand[b]), pt[b, :npn[b]])
+        assert got[b] == want, (b, got[b], want)
+
+
+@pytest.mark.parametrize("V,K,grid", [(2048, 250, False), (2048, 250, True), (2048, 20, False),
+                                      (300, 256, True), (4096, 64, False), (100, 150, False)])
+def test_sample_topk_boundary_draws(gpu, V, K, grid):
+    """Draws placed on the shader's cumulative boundaries: rand equal to a
+    running total (the shader moves past it: rand < total is false), one
+    float below it, and at the last total (the default, the last slot).  The
+    wave-scan totals differ from the shader's single-lane ones in the last
+    bits, so these draws take the kernel's exact fallback; every token must
+    equal the oracle's."""
+    rng = np.random.default_rng(V + K + 7 * grid)
+    base = rng.standard_normal(V) * 2
+    if grid:
+        base = np.round(base * 4) / 4  # tied values as well
+    pt = rng.integers(0, V, size=30).astype(np.uint32)
+    n_pen = 9
+    _, _, cum = oracle.sample_topk_wgsl_detail(base.astype(np.float32), K, 0.8, 1.3, 0.5,
+                                               pt[:n_pen])
+    js = sorted(set(int(j) for j in rng.integers(0, K - 1, size=10)) | {0, K - 2})
+    rands = []
+    for j in js:
+        c = np.float32(cum[j])
+        rands += [c, np.nextafter(c, np.float32(-1)), np.nextafter(c, np.float32(2))]
+    rands += [np.float32(cum[-1]), np.float32(np.nextafter(cum[-1], np.float32(-1)))]
+    rands = np.array([r for r in rands if 0 <= r < 1], np.float32)
+    B = rands.size
+    logits = np.repeat(base.astype(np.float32)[None], B, axis=0)
+    ptb = np.repeat(pt[None], B, axis=0)
+    npn = np.full(B, n_pen, np.uint32)
+    got = host(sts_attn.sample_top_k(dev(logits), K, 0.8, 1.3, dev(rands),
+                                     dev(ptb.view(np.int32)),
+                                     dev(npn.view(np.int32)))).view(np.uint32)
+    for b in range(B):
+        want, _ = oracle.sample_topk_wgsl(logits[b], K, 0.8, 1.3, float(rands[b]), pt[:n_pen])
+        assert got[b] == want, (b, float(rands[b]), got[b], want)
 
 
 def _inputs(cfg, B, seed):
@@ -249,23 +251,28 @@ def _config(cfg):
 
 
 def _check_streams(cfg, w, th, text, rand, pt, npn, tokens, logits, top_k, temp, pen, streams):
-    """Each stream's tokens and logits against the oracle run on that stream."""
-    exact = 0
+    """Each stream's tokens and logits against the oracle run on that stream.
+    Every step's token must be the oracle sampler's on the logits the chain
+    produced (the sampler is exact); the logits must be within 1e-4 of the
+    oracle chain's while the tokens so far agree with the oracle chain's (the
+    GEMMs sum in another f32 order, so a draw within rounding of a boundary
+    may go the other way, after which the streams legitimately part).
+    Returns the number of steps that agreed with the oracle chain."""
+    agree = 0
     for b in streams:
         otok, olog, _ = oracle.depformer_generate(w, th[b], int(text[b]), top_k, temp, pen,
                                                   rand[b], pt[b], npn[b])
-        # Steps up to the first draw that lands within 1e-5 of a boundary
-        # must agree exactly; later steps depend on that draw.
+        same = True
         for s in range(cfg["num_steps"]):
-            np.testing.assert_allclose(logits[s, b], olog[s], rtol=0,
-                                       atol=1e-4 * max(1.0, np.abs(olog[s]).max()))
-            _, safe = _sample_np(olog[s], top_k, temp, pen, float(rand[b, s]),
-                                 pt[b, s, :npn[b, s]])
-            if not safe:
-                break
-            assert tokens[b, s] == otok[s], (b, s)
-            exact += 1
-    return exact
+            want, _ = oracle.sample_topk_wgsl(logits[s, b], top_k, temp, pen, float(rand[b, s]),
+                                              pt[b, s, :npn[b, s]])
+            assert tokens[b, s] == want, (b, s, tokens[b, s], want)
+            if same:
+                np.testing.assert_allclose(logits[s, b], olog[s], rtol=0,
+                                           atol=1e-4 * max(1.0, np.abs(olog[s]).max()))
+                same = tokens[b, s] == otok[s]
+                agree += int(same)
+    return agree
 
 
 def test_depformer_chain_small(gpu):
@@ -372,3 +379,17 @@ def test_depformer_chain_full_shape_and_graph(gpu, full_model):
         np.testing.assert_array_equal(host(t2), host(tokens))
         np.testing.assert_array_equal(host(l2), lg)
     eng.close()
+
+
+def test_sample_topk_tie_known_answers(gpu):
+    """The hand-worked shader cases (see the oracle's known-answer test):
+    [0, 2, 2] with top_k 2 keeps slots [logit 2, logit 1] in that order, so
+    rand 0.25 draws 2 and 0.75 draws 1 (lowest index first would give 1, 2);
+    [1, 1, 2] keeps logit 1, not logit 0, and rand 0.99 draws it."""
+    rows = np.array([[0, 2, 2], [0, 2, 2], [1, 1, 2]], np.float32)
+    rand = np.array([0.25, 0.75, 0.99], np.float32)
+    pt = np.zeros((3, 30), np.int32)
+    npn = np.zeros(3, np.int32)
+    got = host(sts_attn.sample_top_k(dev(rows), 2, 1.0, 1.0, dev(rand), dev(pt),
+                                     dev(npn))).view(np.uint32)
+    assert list(got) == [2, 1, 1]

@@ -225,3 +225,38 @@ def test_chain_planted_mistakes_are_caught(small_model):
     np.testing.assert_array_equal(lb[0], logits[0])   # step 0 does not read audio tables
     dropped = _chain_f64(w, th, 3, tok, drop_residual=True)
     assert np.abs(dropped - logits).max() > 100 * tol
+
+
+def test_sampler_tie_known_answers():
+    """The shader's tie behaviour, worked out by hand from
+    shader_sample_topk.wgsl:134-196 (slots start with logits 0..K-1; a logit
+    strictly above the minimum replaces the first slot holding it; the
+    insertion sort is stable, so equal values keep slot order), where it
+    differs from 'lowest index first':
+      [0, 2, 2], K=2: slot 0 (value 0) takes logit 2 -> slots [2 (i2), 2 (i1)],
+        sorted i2 then i1, each weight 1/2: rand 0.25 -> 2, rand 0.75 -> 1.
+      [1, 1, 2], K=2: logit 2 replaces slot 0 -> [2 (i2), 1 (i1)]: logit 1 is
+        kept, not logit 0; rand 0.99 -> 1.
+    Temperature 1, no penalty."""
+    lg = np.array([0, 2, 2], np.float32)
+    assert oracle.sample_topk_wgsl(lg, 2, 1.0, 1.0, 0.25)[0] == 2
+    assert oracle.sample_topk_wgsl(lg, 2, 1.0, 1.0, 0.75)[0] == 1
+    tok, idx, cum = oracle.sample_topk_wgsl_detail(lg, 2, 1.0, 1.0, 0.25)
+    assert list(idx) == [2, 1] and cum[0] == np.float32(0.5)
+    lg = np.array([1, 1, 2], np.float32)
+    tok, idx, _ = oracle.sample_topk_wgsl_detail(lg, 2, 1.0, 1.0, 0.99)
+    assert list(idx) == [2, 1] and tok == 1
+
+
+def test_sampler_draw_on_a_boundary():
+    """rand < running total picks the slot, so rand equal to a total moves to
+    the next slot, and rand at or past the last total takes the last slot."""
+    rng = np.random.default_rng(5)
+    lg = rng.standard_normal(300).astype(np.float32)
+    _, idx, cum = oracle.sample_topk_wgsl_detail(lg, 40, 0.9, 1.0, 0.5)
+    assert np.all(np.diff(cum) >= 0)
+    for j in (0, 7, 38):
+        assert oracle.sample_topk_wgsl(lg, 40, 0.9, 1.0, float(cum[j]))[0] == idx[j + 1]
+        below = float(np.nextafter(cum[j], np.float32(-1)))
+        assert oracle.sample_topk_wgsl(lg, 40, 0.9, 1.0, below)[0] == idx[j]
+    assert oracle.sample_topk_wgsl(lg, 40, 0.9, 1.0, float(cum[-1]))[0] == idx[-1]
