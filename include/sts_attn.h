@@ -223,6 +223,8 @@ typedef struct sts_rope sts_rope;
  * current device (synchronous, once).
  */
 int sts_rope_create(uint32_t head_dim, uint32_t max_seq_len, float theta, sts_rope** out);
+/* Frees the tables (hipFree): not while a stream of the device is being
+ * captured into a graph, which a free inside the capture would invalidate. */
 int sts_rope_destroy(sts_rope* rope);
 
 /*
@@ -294,6 +296,8 @@ int sts_kv_sync_mirror(sts_kv_cache* cache, void* stream);
  * is q_heads = heads.
  */
 int sts_kv_set_query_heads(sts_kv_cache* cache, uint64_t q_heads);
+/* Frees the buffers (hipFree): not while a stream of the device is being
+ * captured into a graph, which a free inside the capture would invalidate. */
 int sts_kv_destroy(sts_kv_cache* cache);
 
 /*

@@ -261,10 +261,44 @@ def prefill_attention_bf16kv(q: torch.Tensor, k16: torch.Tensor, v16: torch.Tens
 # RoPE
 # ---------------------------------------------------------------------------
 
+# Handles whose Python object was released while the current stream was being
+# captured into a graph: destroying them then would free device memory inside
+# the capture (which invalidates it), so they are destroyed by the next handle
+# release or creation outside a capture.
+_deferred = []
+
+
+def _capturing() -> bool:
+    try:
+        return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+    except Exception:
+        return False
+
+
+def _release(destroy, handle) -> None:
+    """Destroys `handle` with `destroy` (a library entry point), or defers it
+    while the current stream is being captured; runs deferred ones when it can."""
+    if _capturing():
+        _deferred.append((destroy, handle))
+        return
+    while _deferred:
+        d, h = _deferred.pop()
+        getattr(load(), d)(h)
+    getattr(load(), destroy)(handle)
+
+
+def _drain_deferred() -> None:
+    if _deferred and not _capturing():
+        while _deferred:
+            d, h = _deferred.pop()
+            getattr(load(), d)(h)
+
+
 class RoPE:
     """RoPE::new / apply (model.rs:44-121) with tables held by the library."""
 
     def __init__(self, head_dim: int, max_seq_len: int, theta: float = 10000.0):
+        _drain_deferred()
         h = _vp()
         _check(load().sts_rope_create(head_dim, max_seq_len, theta, ctypes.byref(h)))
         self._h = h
@@ -288,7 +322,7 @@ class RoPE:
 
     def close(self):
         if self._h:
-            load().sts_rope_destroy(self._h)
+            _release("sts_rope_destroy", self._h)
             self._h = _vp()
 
     def __del__(self):
@@ -309,6 +343,7 @@ class KVCache:
                  n_heads: Optional[int] = None):
         """n_heads: query heads when they outnumber the K/V heads (grouped-query
         attention, model.rs:766-783); q and out then have n_heads heads."""
+        _drain_deferred()
         h = _vp()
         _check(load().sts_kv_create_ex(max_len, n_kv_heads, head_dim,
                                        KV_BF16_MIRROR if bf16_mirror else 0, ctypes.byref(h)))
@@ -431,7 +466,7 @@ class KVCache:
 
     def close(self):
         if self._h:
-            load().sts_kv_destroy(self._h)
+            _release("sts_kv_destroy", self._h)
             self._h = _vp()
 
     def __del__(self):

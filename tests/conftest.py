@@ -17,6 +17,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library on cuda:0)")
 
 
+@pytest.fixture(autouse=True)
+def _gc_between_tests():
+    """Cyclic garbage is collected between tests, never at an arbitrary point
+    inside one: the library's handles free device memory when collected, and a
+    free while a stream is being captured into a graph invalidates the capture."""
+    import gc
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
+        gc.collect()
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The HIP library on cuda:0.  Fails (never skips) when no GPU is present."""
