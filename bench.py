@@ -260,6 +260,27 @@ def bench_prefill(torch, sts, stream, steps, warmup):
     us_layer = t.ms * 1e3 / steps / LAYERS
     res["bf16kv"] = {"us_per_layer": us_layer,
                      "tflops": flops_layer / (us_layer * 1e-6) / 1e12}
+    # The f32-input bf16 kernel with fewer cached rows before the same 512
+    # queries: the longest query tile then streams 8..11 key blocks instead
+    # of 12 (all other tiles one to four fewer too).  How the layer time
+    # follows the longest tile's blocks bounds what balancing the tiles could
+    # gain at config 3 (8.5 blocks per tile on average).
+    scan = {}
+    for c in (0, 64, 128, 192):
+        Lc = c + S
+
+        def run_c():
+            for layer in range(LAYERS):
+                sts.prefill_attention(q[layer], kc[layer], vc[layer], starts[layer], Lc, scale,
+                                      sts.PREC_BF16_MFMA, out=out[layer], stream=stream)
+        for _ in range(min(warmup, 10)):
+            run_c()
+        with Timer(torch, stream) as t:
+            for _ in range(steps):
+                run_c()
+        scan[(Lc + 63) // 64] = t.ms * 1e3 / steps / LAYERS
+    scan[(L + 63) // 64] = res["bf16"]["us_per_layer"]
+    res["bf16_scan"] = scan
     # Algorithmic HBM bytes per layer: K/V rows of the window (f32, or bf16
     # for the mirror), Q read and O written (f32).
     qo = 2 * S * H * D * 4
@@ -802,7 +823,12 @@ def main():
             "bf16kv_us_per_layer": round(p["bf16kv"]["us_per_layer"], 3),
             "bf16kv_tflops": round(p["bf16kv"]["tflops"], 1),
             "bf16kv_frac_of_hbm_roof": round(p["bytes_bf16kv"] / (HBM_PEAK_GBS * 1e3)
-                                             / p["bf16kv"]["us_per_layer"], 4)}
+                                             / p["bf16kv"]["us_per_layer"], 4),
+            # us per layer of the f32-input bf16 kernel at 512 queries after
+            # 0, 64, 128, 192 and 256 cached rows, keyed by the key blocks of
+            # the longest query tile (8 .. 12; 12 is config 3).
+            "bf16_us_by_longest_tile_blocks": {str(k): round(v, 3)
+                                               for k, v in sorted(p["bf16_scan"].items())}}
     if "depformer" in extra:
         line["depformer"] = {k: round(v, 3) for k, v in extra["depformer"].items()}
     if "ragged" in extra:

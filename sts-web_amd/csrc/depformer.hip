@@ -589,12 +589,13 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   // sort (:134-196) whenever no two of the logits the order depends on are
   // equal.
   uint64_t key = rank_keys();
-  bool emulated = false;
+  bool tied = false;
   if (V > K) {
     // Ties: two of the K taken with equal values (the stable insertion sort
     // orders them by the shader's slot, not by index), or a logit left out
     // with the value of the K-th (which of those the shader keeps depends on
-    // its slots).  Then wave 0 replays the shader's selection itself.
+    // its slots).  Either changes only which index stands at the ranks of
+    // the equal values, never the values at any rank.
     const uint32_t tkey = (uint32_t)(sbuf[256 + K - 1] >> 32);
     bool tie = tid + 1 < K && (uint32_t)(sbuf[256 + tid + 1] >> 32) == (uint32_t)(key >> 32);
     uint32_t n_ge = 0;
@@ -605,82 +606,12 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
     if (n_ge) atomicAdd(&s_tie[0], n_ge);
     if (tie) s_tie[1] = 1;
     __syncthreads();
-    emulated = s_tie[1] != 0 || s_tie[0] > K;
-  }
-  if (emulated) {
-    // The logits' keys in index order (vals is free once the keys exist).
-    uint32_t* lk = reinterpret_cast<uint32_t*>(vals);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (tid + 256u * j < V) lk[tid + 256u * j] = k[j];
-    if (tid >= K) ck[tid] = 0;
-    __syncthreads();
-    if (wave == 0) {
-      // Slot s = lane + 64c holds (key << 32 | s) and its logit's index.
-      // Thread 0's loop (:148-178): slots 0..K-1 start with logits 0..K-1;
-      // logit j >= K replaces the first slot holding the minimum when it is
-      // strictly greater, and the minimum is found again.
-      uint64_t sk[4];
-      uint32_t sidx[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t sl = lane + 64u * c;
-        sk[c] = sl < K ? ((uint64_t)lk[sl] << 32) | sl : ~0ull;
-        sidx[c] = sl;
-      }
-      auto wave_min = [&]() {
-        uint64_t m = sk[0];
-#pragma unroll
-        for (int c = 1; c < 4; ++c) m = sk[c] < m ? sk[c] : m;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t lo = __shfl_xor((uint32_t)m, off, 64);
-          const uint32_t hi = __shfl_xor((uint32_t)(m >> 32), off, 64);
-          const uint64_t o = ((uint64_t)hi << 32) | lo;
-          m = o < m ? o : m;
-        }
-        return m;
-      };
-      uint64_t mn = wave_min();
-      for (uint32_t j0 = K; j0 < V; j0 += 64) {
-        const uint32_t j = j0 + lane;
-        const bool in = j < V;
-        const uint32_t kj = in ? lk[j] : 0u;
-        uint64_t bits = __ballot(in && kj > (uint32_t)(mn >> 32));
-        while (bits) {
-          const int bl = __builtin_ctzll(bits);
-          const uint32_t kb = __builtin_amdgcn_readlane(kj, bl);
-          const uint32_t sl = (uint32_t)mn;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (lane + 64u * c == sl) {
-              sk[c] = ((uint64_t)kb << 32) | sl;
-              sidx[c] = j0 + (uint32_t)bl;
-            }
-          mn = wave_min();
-          bits &= ~((2ull << bl) - 1ull);
-          bits &= __ballot(in && kj > (uint32_t)(mn >> 32));
-        }
-      }
-      // Ranked as the insertion sort orders them: value descending, slot
-      // ascending among equal values.
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t sl = lane + 64u * c;
-        if (sl < K) {
-          ck[sl] = (sk[c] & 0xFFFFFFFF00000000ull) | (0xFFFFFFFFu - sl);
-          slot_idx[sl] = sidx[c];
-        }
-      }
-    }
-    __syncthreads();
-    key = rank_keys();
+    tied = s_tie[1] != 0 || s_tie[0] > K;
   }
   // K > V: the shader's unused slots hold (-3.402823466e+38, 0).
   const bool real = tid < Ks;
   const float v = real ? key_value((uint32_t)(key >> 32)) : -3.402823466e+38f;
-  const uint32_t low = 0xFFFFFFFFu - (uint32_t)key;
-  ri[tid] = real ? (emulated ? slot_idx[low] : low) : 0u;
+  ri[tid] = real ? 0xFFFFFFFFu - (uint32_t)key : 0u;
   if (tid == 0) s_maxv = v;
   __syncthreads();
   // Softmax over the K (:198-210): exp(v - max) correctly rounded to f32
@@ -767,8 +698,97 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
         }
       }
     }
-    if (tid == 0) *outp = ri[pick];
+    if (tid == 0) {
+      // The draw picked a rank (the values by rank, and so the draw, are the
+      // same whatever order equal values take).  Only a rank whose value
+      // another rank among the K shares, or the K-th value when more logits
+      // share it than were taken, can hold a different index in the shader.
+      bool need = false;
+      if (tied) {
+        const uint32_t vp = (uint32_t)(sbuf[256 + pick] >> 32);
+        need = (pick > 0 && (uint32_t)(sbuf[256 + pick - 1] >> 32) == vp) ||
+               (pick + 1 < K && (uint32_t)(sbuf[256 + pick + 1] >> 32) == vp) ||
+               (s_tie[0] > K && vp == (uint32_t)(sbuf[256 + K - 1] >> 32));
+      }
+      s_tie[1] = pick;
+      s_tie[0] = need ? 1u : 0u;
+      if (!need) *outp = ri[pick];
+    }
   }
+  __syncthreads();
+  if (s_tie[0] == 0) return;
+  const uint32_t pick = s_tie[1];
+  // Then the shader's selection is replayed: wave 0 runs its loop over the
+  // logits' keys in index order (vals is free once the keys exist), the
+  // slots are ranked as its stable insertion sort ranks them, and the index
+  // at the drawn rank is the token.
+  uint32_t* lk = reinterpret_cast<uint32_t*>(vals);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (tid + 256u * j < V) lk[tid + 256u * j] = k[j];
+  if (tid >= K) ck[tid] = 0;
+  __syncthreads();
+  if (wave == 0) {
+    // Slot s = lane + 64c holds (key << 32 | s) and its logit's index.
+    // Thread 0's loop (:148-178): slots 0..K-1 start with logits 0..K-1;
+    // logit j >= K replaces the first slot holding the minimum when it is
+    // strictly greater, and the minimum is found again.
+    uint64_t sk[4];
+    uint32_t sidx[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t sl = lane + 64u * c;
+      sk[c] = sl < K ? ((uint64_t)lk[sl] << 32) | sl : ~0ull;
+      sidx[c] = sl;
+    }
+    auto wave_min = [&]() {
+      uint64_t m = sk[0];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) m = sk[c] < m ? sk[c] : m;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)m, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(m >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        m = o < m ? o : m;
+      }
+      return m;
+    };
+    uint64_t mn = wave_min();
+    for (uint32_t j0 = K; j0 < V; j0 += 64) {
+      const uint32_t j = j0 + lane;
+      const bool in = j < V;
+      const uint32_t kj = in ? lk[j] : 0u;
+      uint64_t bits = __ballot(in && kj > (uint32_t)(mn >> 32));
+      while (bits) {
+        const int bl = __builtin_ctzll(bits);
+        const uint32_t kb = __builtin_amdgcn_readlane(kj, bl);
+        const uint32_t sl = (uint32_t)mn;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (lane + 64u * c == sl) {
+            sk[c] = ((uint64_t)kb << 32) | sl;
+            sidx[c] = j0 + (uint32_t)bl;
+          }
+        mn = wave_min();
+        bits &= ~((2ull << bl) - 1ull);
+        bits &= __ballot(in && kj > (uint32_t)(mn >> 32));
+      }
+    }
+    // Ranked as the insertion sort orders them: value descending, slot
+    // ascending among equal values.
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t sl = lane + 64u * c;
+      if (sl < K) {
+        ck[sl] = (sk[c] & 0xFFFFFFFF00000000ull) | (0xFFFFFFFFu - sl);
+        slot_idx[sl] = sidx[c];
+      }
+    }
+  }
+  __syncthreads();
+  key = rank_keys();
+  if (tid == pick) *outp = slot_idx[0xFFFFFFFFu - (uint32_t)key];
 }
 
 // y[m][n] = sum over the slices s of part[s][m][n] in slice order, plus

@@ -229,6 +229,49 @@ def test_sample_topk_boundary_draws(gpu, V, K, grid):
         assert got[b] == want, (b, float(rands[b]), got[b], want)
 
 
+@pytest.mark.parametrize("case", ["pair_in_top_k", "pair_at_kth"])
+def test_sample_topk_rare_ties(gpu, case):
+    """Distinct logits but one pair of equal values, as f32 logits of a real
+    chain have now and then: the pair among the top K, or a logit left out
+    equal to the K-th.  Draws land in the middle of the pair's ranks (the
+    shader's selection and sort decide which index stands there) and of ranks
+    elsewhere (any order of the pair gives the same token there); every token
+    equals the oracle's."""
+    V, K = 2048, 250
+    rng = np.random.default_rng(11 if case == "pair_in_top_k" else 12)
+    base = (rng.standard_normal(V) * 2).astype(np.float32)
+    order = np.argsort(-base, kind="stable")
+    if case == "pair_in_top_k":
+        lo, hi = sorted(int(i) for i in order[[7, 31]])
+        base[hi] = base[lo]          # equal values at two adjacent ranks
+    else:
+        kth, out = int(order[K - 1]), int(order[K + 9])
+        base[out] = base[kth]        # a logit left out ties with the K-th
+    _, idx, cum = oracle.sample_topk_wgsl_detail(base, K, 0.8, 1.0, 0.5)
+    vals = base[idx] / np.float32(0.8)
+    if case == "pair_in_top_k":
+        tied = [r for r in range(K) if (r > 0 and vals[r - 1] == vals[r]) or
+                (r + 1 < K and vals[r + 1] == vals[r])]
+    else:
+        tied = [r for r in range(K) if base[idx[r]] == base[out]]
+    ranks = sorted(set(tied) | {0, 3, 100, K - 2, K - 1})
+    # The shader's order at the tie is not index order (so the test tells a
+    # replay from the index-ordered ranking): seeds and ranks chosen for it.
+    assert tied and any(idx[r] > idx[r + 1] for r in tied[:-1]) or \
+        (case == "pair_at_kth" and idx[K - 1] == out and out > kth)
+    lows = np.concatenate([[0.0], cum[:-1]])
+    rands = np.array([(lows[r] + cum[r]) / 2 for r in ranks], np.float32)
+    B = rands.size
+    logits = np.repeat(base[None], B, axis=0)
+    pt = np.zeros((B, 30), np.int32)
+    npn = np.zeros(B, np.int32)
+    got = host(sts_attn.sample_top_k(dev(logits), K, 0.8, 1.0, dev(rands), dev(pt),
+                                     dev(npn))).view(np.uint32)
+    for b in range(B):
+        want, _ = oracle.sample_topk_wgsl(base, K, 0.8, 1.0, float(rands[b]))
+        assert got[b] == want, (case, ranks[b], got[b], want)
+
+
 def _inputs(cfg, B, seed):
     S = cfg["num_steps"]
     th = oracle.normal(seed, (B, cfg["temporal_dim"]))
