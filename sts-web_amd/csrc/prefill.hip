@@ -68,6 +68,14 @@ __device__ __forceinline__ float4 load_query4(const PrefillParams& p, const floa
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// Output rows are written once and not read in the launch: nontemporal
+// stores keep them from pushing out of L2 the K/V blocks that the longer
+// tiles of a head read after the shorter tiles have finished (512 queries
+// after 256 cached, f32 K/V: 19.4 -> 18.4 us per layer in the bf16 kernel,
+// 56.6 -> 55.9 us in the f32 one).
+__device__ __forceinline__ void st4_stream(float* p, float4 v) {
+  __builtin_nontemporal_store(coh_f4{v.x, v.y, v.z, v.w}, reinterpret_cast<coh_f4*>(p));
+}
 __device__ __forceinline__ float4 scale4(float4 x, float c) {
   return make_float4(x.x * c, x.y * c, x.z * c, x.w * c);
 }
@@ -405,7 +413,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
         r.y = o[t][1] / lsum;
         r.z = o[t][2] / lsum;
         r.w = o[t][3] / lsum;
-        *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) = r;
+        st4_stream(orow + 16 * t + 4 * g, r);
       }
     }
     return;
@@ -488,7 +496,7 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
         r.y = acc[t][1] / l;
         r.z = acc[t][2] / l;
         r.w = acc[t][3] / l;
-        *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) = r;
+        st4_stream(orow + 16 * t + 4 * g, r);
       }
     }
   }
@@ -1127,7 +1135,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       y.y = (o[t][4 * r + 1] * f1 + src[16 * t + 4 * r + 1] * f2) * inv;
       y.z = (o[t][4 * r + 2] * f1 + src[16 * t + 4 * r + 2] * f2) * inv;
       y.w = (o[t][4 * r + 3] * f1 + src[16 * t + 4 * r + 3] * f2) * inv;
-      *reinterpret_cast<float4*>(orow + 32 * t + 8 * r + 4 * hh) = y;
+      st4_stream(orow + 32 * t + 8 * r + 4 * hh, y);
     }
 }
 
