@@ -30,6 +30,8 @@
 // of the longest visit their key blocks last to first, ending on the blocks
 // every tile of the head shares (by then in L2); on the bf16-mirror path the
 // shorter tiles also start staggered when all tiles are resident at once.
+// Both kernels write the output rows with nontemporal stores, which keep the
+// finished tiles' output from pushing those shared blocks out of L2.
 #include <algorithm>
 #include <cfloat>
 
