@@ -381,7 +381,7 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   __shared__ __align__(16) float ev[kMaxTopK];
   __shared__ uint32_t ri[kMaxTopK];
   __shared__ float s_maxv;
-  __shared__ uint32_t s_ptok[kMaxPenalty];
+  __shared__ uint32_t s_pbits[4096 / 32];  // the listed penalty tokens, one bit each
   __shared__ uint64_t sbuf[2 * kMaxTopK];
   __shared__ uint32_t slot_idx[kMaxTopK];  // replayed selection: slot -> logit index
   __shared__ uint32_t s_tie[2];            // keys >= the K-th, any equal neighbours
@@ -404,28 +404,20 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   hist[0][tid] = 0;
   hist[1][tid] = 0;
 
-  // Repetition penalty (:56-69); a token listed twice is penalised once.
+  // Repetition penalty (:56-69); a token listed twice is penalised once (the
+  // shader's lanes all read before they write).  The listed tokens set their
+  // bits in an LDS bitmap, and each thread penalises the logits it holds.
+  static_assert(NJ * 256 <= 4096, "penalty bitmap");
   if (np > 0) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const uint32_t i = tid + 256u * j;
-      if (i < V) vals[i] = x[j];
-    }
-    if (tid < np) s_ptok[tid] = tok;
+    if (tid < 4096 / 32) s_pbits[tid] = 0;
     __syncthreads();
-    if (tid < np) {
-      bool dup = false;
-      for (uint32_t q = 0; q < tid; ++q) dup |= s_ptok[q] == tok;
-      if (!dup && tok < V) {
-        const float v = vals[tok];
-        vals[tok] = v > 0.f ? v / p.penalty : v * p.penalty;
-      }
-    }
+    if (tid < np && tok < V) atomicOr(&s_pbits[tok >> 5], 1u << (tok & 31u));
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const uint32_t i = tid + 256u * j;
-      if (i < V) x[j] = vals[i];
+      if (i < V && ((s_pbits[i >> 5] >> (i & 31u)) & 1u))
+        x[j] = x[j] > 0.f ? x[j] / p.penalty : x[j] * p.penalty;
     }
   }
   // Temperature (:72-88).
@@ -669,34 +661,35 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
                               (pick == 0 || rnd >= cumv[pick - 1] + kDrawSlack))
                            : rnd >= cumv[K - 1] + kDrawSlack;
     if (!sure) {
-      // The shader's order: sum in slot order on one lane, each weight
-      // divided by it, the running total in slot order.
-      if (tid == 0) {
-        float sq = 0.f;
-        for (uint32_t j = 0; j < K; ++j) sq = sq + ev[j];
-        s_maxv = sq;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const float sq = s_maxv;
+      // The shader's order: the sum in slot order, each weight divided by
+      // it, the running total in slot order.  The wave computes both as one
+      // uniform chain, slot 4l + c read from lane l's registers (the slots
+      // past K hold +0, which leaves a sum unchanged).
+      auto lane_f = [](float x, int l) {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+      };
+      float sq = 0.f;
+      for (int l = 0; l < 64; ++l)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (4 * tid + c < K) cumv[4 * tid + c] = e[c] / sq;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (tid == 0) {
-        float cum = 0.f;
-        pick = K - 1;
-        for (uint32_t j = 0; j < K; ++j) {
-          cum = cum + cumv[j];
-          if (rnd < cum) {
-            pick = j;
-            break;
+        for (int c = 0; c < 4; ++c) sq = sq + lane_f(e[c], l);
+      float w[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w[c] = e[c] / sq;
+      float cum = 0.f;
+      pick = K - 1;
+      bool found = false;
+      for (int l = 0; l < 64 && !found; ++l)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t j = 4u * l + c;
+          if (!found && j < K) {
+            cum = cum + lane_f(w[c], l);
+            if (rnd < cum) {
+              pick = j;
+              found = true;
+            }
           }
         }
-      }
     }
     if (tid == 0) {
       // The draw picked a rank (the values by rank, and so the draw, are the
