@@ -394,6 +394,7 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   // The logits first; the penalty tokens once their count is in (only that
   // many are guaranteed readable).
   const uint32_t np = min(p.num_penalty[(size_t)b * p.rs_stride], kMaxPenalty);
+  const float rnd = p.rand[(size_t)b * p.rs_stride];  // the draw's, requested now
   float x[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -593,9 +594,10 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
     uint32_t n_ge = 0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) n_ge += (tid + 256u * j < V && k[j] >= tkey) ? 1u : 0u;
+    n_ge = __builtin_amdgcn_readlane(wave_scan_incl(n_ge), 63);  // the wave's total
     if (tid == 0) s_tie[0] = s_tie[1] = 0;
     __syncthreads();
-    if (n_ge) atomicAdd(&s_tie[0], n_ge);
+    if (lane == 0 && n_ge) atomicAdd(&s_tie[0], n_ge);
     if (tie) s_tie[1] = 1;
     __syncthreads();
     tied = s_tie[1] != 0 || s_tie[0] > K;
@@ -641,7 +643,6 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       if (4 * tid + c < K) cumv[4 * tid + c] = pre + q[c];
-    const float rnd = p.rand[(size_t)b * p.rs_stride];
     int first = 4;
 #pragma unroll
     for (int c = 3; c >= 0; --c)
