@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   __shared__ uint64_t sbuf[2 * kMaxTopK];
   __shared__ uint32_t slot_idx[kMaxTopK];  // replayed selection: slot -> logit index
   __shared__ uint32_t s_tie[2];            // keys >= the K-th, any equal neighbours
-  __shared__ float cumv[kMaxTopK];         // running totals (or weights) of the draw
+  __shared__ __align__(16) float cumv[kMaxTopK];  // the scan's running totals, then the weights
   static_assert(kMaxTopK == 256, "one key per thread in the ranking sort");
   const uint32_t tid = threadIdx.x, b = blockIdx.x, V = p.V;
   const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -611,7 +611,7 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
   // Softmax over the K (:198-210): exp(v - max) correctly rounded to f32
   // (through f64), the rounding the oracle takes for WGSL's exp.
   const float max_v = s_maxv;
-  if (tid < K) ev[tid] = (float)exp((double)(v - max_v));
+  ev[tid] = tid < K ? (float)exp((double)(v - max_v)) : 0.f;  // +0 past K
   __syncthreads();
   if (tid < 64) {
     // The cumulative draw (:212-221).  Wave 0: lane l holds values 4l..4l+3;
@@ -663,34 +663,52 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
                            : rnd >= cumv[K - 1] + kDrawSlack;
     if (!sure) {
       // The shader's order: the sum in slot order, each weight divided by
-      // it, the running total in slot order.  The wave computes both as one
-      // uniform chain, slot 4l + c read from lane l's registers (the slots
-      // past K hold +0, which leaves a sum unchanged).
-      auto lane_f = [](float x, int l) {
-        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
-      };
+      // it, the running total in slot order.  Both chains run on lane 0 over
+      // 16 values at a time from LDS (the loads ahead of the additions; the
+      // slots past K hold +0, which leaves a sum unchanged), the divisions on
+      // every lane in between.
       float sq = 0.f;
-      for (int l = 0; l < 64; ++l)
+      if (tid == 0) {
+        for (uint32_t j0 = 0; j0 < K; j0 += 16) {
+          float4 t[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) sq = sq + lane_f(e[c], l);
-      float w[4];
+          for (int q4 = 0; q4 < 4; ++q4) t[q4] = *reinterpret_cast<const float4*>(&ev[j0 + 4 * q4]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) w[c] = e[c] / sq;
-      float cum = 0.f;
-      pick = K - 1;
-      bool found = false;
-      for (int l = 0; l < 64 && !found; ++l)
+          for (int q4 = 0; q4 < 4; ++q4) {
+            sq = sq + t[q4].x;
+            sq = sq + t[q4].y;
+            sq = sq + t[q4].z;
+            sq = sq + t[q4].w;
+          }
+        }
+      }
+      sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t j = 4u * l + c;
-          if (!found && j < K) {
-            cum = cum + lane_f(w[c], l);
-            if (rnd < cum) {
-              pick = j;
+      for (int c = 0; c < 4; ++c) cumv[4 * tid + c] = e[c] / sq;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint32_t pk = K - 1;
+      if (tid == 0) {
+        float cum = 0.f;
+        bool found = false;
+        for (uint32_t j0 = 0; j0 < K && !found; j0 += 16) {
+          float4 t[4];
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) t[q4] = *reinterpret_cast<const float4*>(&cumv[j0 + 4 * q4]);
+          const float w[16] = {t[0].x, t[0].y, t[0].z, t[0].w, t[1].x, t[1].y, t[1].z, t[1].w,
+                               t[2].x, t[2].y, t[2].z, t[2].w, t[3].x, t[3].y, t[3].z, t[3].w};
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            cum = cum + w[i];
+            if (!found && j0 + i < K && rnd < cum) {
+              pk = j0 + i;
               found = true;
             }
           }
         }
+      }
+      pick = __builtin_amdgcn_readfirstlane(pk);
     }
     if (tid == 0) {
       // The draw picked a rank (the values by rank, and so the draw, are the
