@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "depformer.hpp"
@@ -753,16 +754,35 @@ __global__ __launch_bounds__(256) void sample_topk_kernel(const SampleParams p) 
       sk[c] = sl < K ? ((uint64_t)lk[sl] << 32) | sl : ~0ull;
       sidx[c] = sl;
     }
+    // The wave's minimum in every lane: partners within quads (DPP quad
+    // permutations), mirrored within 8 and 16 lanes (DPP), then across 16
+    // and 32 lanes (permlane swaps) -- register exchanges only.
     auto wave_min = [&]() {
       uint64_t m = sk[0];
 #pragma unroll
       for (int c = 1; c < 4; ++c) m = sk[c] < m ? sk[c] : m;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)m, off, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(m >> 32), off, 64);
+      auto dpp_min = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)m, C, 0xF, 0xF, false);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(m >> 32), C, 0xF, 0xF, false);
         const uint64_t o = ((uint64_t)hi << 32) | lo;
         m = o < m ? o : m;
+      };
+      dpp_min(std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+      dpp_min(std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+      dpp_min(std::integral_constant<int, 0x141>{});  // row_half_mirror
+      dpp_min(std::integral_constant<int, 0x140>{});  // row_mirror
+      {
+        const auto l2 = __builtin_amdgcn_permlane16_swap((uint32_t)m, (uint32_t)m, false, false);
+        const auto h2 = __builtin_amdgcn_permlane16_swap((uint32_t)(m >> 32), (uint32_t)(m >> 32), false, false);
+        const uint64_t a = ((uint64_t)h2[0] << 32) | l2[0], c = ((uint64_t)h2[1] << 32) | l2[1];
+        m = a < c ? a : c;
+      }
+      {
+        const auto l2 = __builtin_amdgcn_permlane32_swap((uint32_t)m, (uint32_t)m, false, false);
+        const auto h2 = __builtin_amdgcn_permlane32_swap((uint32_t)(m >> 32), (uint32_t)(m >> 32), false, false);
+        const uint64_t a = ((uint64_t)h2[0] << 32) | l2[0], c = ((uint64_t)h2[1] << 32) | l2[1];
+        m = a < c ? a : c;
       }
       return m;
     };
