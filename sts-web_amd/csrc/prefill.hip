@@ -609,7 +609,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   constexpr int VPER = VSQ >= NP ? VSQ / NP : 1;
   static_assert(KPER >= 1 && (VSQ % NP == 0 || NP % VSQ == 0), "tile shape");
   __shared__ Stage st[NS];
-  __shared__ uint32_t filled[NS], released[NS], q_ready;
+  __shared__ uint32_t filled[NS], vfilled[NS], released[NS], q_ready;
   // The tile's queries, scaled and rounded to bf16 once by the producers
   // (each query row is the B operand of two consumer waves).
   constexpr int QP = D + 8;  // row pitch (bf16)
@@ -639,6 +639,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
   auto blk = [&](uint32_t i) { return reverse && i < nblk ? nblk - 1 - i : i; };
   if (tid < NS) {
     filled[tid] = 0;
+    vfilled[tid] = 0;
     released[tid] = 0;
     if (tid == 0) q_ready = 0;
   }
@@ -737,10 +738,12 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     };
     // K chunks go to their rows as they are; each V piece (4 keys x 8 dims) is
     // transposed into 8 runs of 4 keys (dims c8*8 .. +7).
-    auto put = [&](const Buf& bf, Stage& sg) {
+    auto put_k = [&](const Buf& bf, Stage& sg) {
 #pragma unroll
       for (int i = 0; i < KP16; ++i)
         *reinterpret_cast<u32x4*>(&sg.ks[0][k_row(i) * KP + c8 * 8]) = bf.k[i];
+    };
+    auto put_v = [&](const Buf& bf, Stage& sg) {
       if (!v_thread) return;
 #pragma unroll
       for (int i = 0; i < VP16; ++i) {
@@ -761,8 +764,14 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     auto produce = [&](const Buf& bf, uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane, p.err);
-      put(bf, st[s]);
-      ws_signal(&filled[s], lane);
+      // The split kernel's consumers (its three products per block make them
+      // the slower side) may start the scores once K is in (vfilled then
+      // counts V); elsewhere one signal covers the block (two measured
+      // slower there).
+      put_k(bf, st[s]);
+      if constexpr (SPLIT) ws_signal(&filled[s], lane);
+      put_v(bf, st[s]);
+      ws_signal(SPLIT ? &vfilled[s] : &filled[s], lane);
     };
     // Queries: as the f32 producers stage them.
     constexpr int QPER = QT * C4 / NP;
@@ -888,12 +897,14 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         (void)lo_plane;
       }
     };
-    auto put = [&](const Buf& bf, Stage& sg) {
+    auto put_k = [&](const Buf& bf, Stage& sg) {
 #pragma unroll
       for (int i = 0; i < KPER; ++i) {
         const floatx4 x = bf.k[i];
         store4(sg.ks[0], sg.ks[Stage::NPL - 1], k_row(i) * KP + d4 * 4, x.x, x.y, x.z, x.w);
       }
+    };
+    auto put_v = [&](const Buf& bf, Stage& sg) {
       if (!v_thread) return;
 #pragma unroll
       for (int i = 0; i < VPER; ++i) {
@@ -911,8 +922,10 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     auto produce = [&](const Buf& bf, uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&released[s], 4 * use, p.wait_limit, lane, p.err);
-      put(bf, st[s]);
-      ws_signal(&filled[s], lane);
+      put_k(bf, st[s]);
+      if constexpr (SPLIT) ws_signal(&filled[s], lane);
+      put_v(bf, st[s]);
+      ws_signal(SPLIT ? &vfilled[s] : &filled[s], lane);
     };
     // Three blocks in flight in registers: block i is converted and stored
     // while blocks i+1 and i+2 load (the per-CU load rate, not the issue,
@@ -1074,6 +1087,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         }
       // V^T operands are read per output tile after the softmax (the stage
       // stays claimed until they are in registers), then the stage is released.
+      if constexpr (SPLIT) ws_wait_ge(&vfilled[s], 4 * (i / NS + 1), p.wait_limit, lane, p.err);
 #pragma unroll
       for (int t = 0; t < OT; ++t) {
 #pragma unroll
