@@ -198,28 +198,45 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   const int jj = (c >> 2) & (RPG - 1);
 
-  // Loads rows r0 + j*NG + g (j < RPG) of this lane's group into kk/vv.
+  // Byte offset of window row r in this lane's K/V resource (rows outside the
+  // window get an offset past it and load zeros).
+  auto row_off = [&](uint32_t r) {
+    uint32_t slot = start + r;
+    slot = slot >= p.M ? slot - p.M : slot;
+    return r < len && lane_ok ? slot * (dh * (uint32_t)sizeof(float)) + c * 16 : 0x80000000u;
+  };
+  // Rows r0 + j*NG + g (j < RPG) of this lane's group: K into kk, V into vv,
+  // or both, K and V of each row together.
+  auto load_k = [&](uint32_t r0, float4* kk) {
+#pragma unroll
+    for (int j = 0; j < RPG; ++j)
+      kk[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             krs, row_off(r0 + j * NG + g), 0, kNt));
+  };
+  auto load_v = [&](uint32_t r0, float4* vv) {
+#pragma unroll
+    for (int j = 0; j < RPG; ++j)
+      vv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             vrs, row_off(r0 + j * NG + g), 0, kNt));
+  };
   auto load_rows = [&](uint32_t r0, float4* kk, float4* vv) {
 #pragma unroll
     for (int j = 0; j < RPG; ++j) {
-      const uint32_t r = r0 + j * NG + g;
-      uint32_t slot = start + r;
-      slot = slot >= p.M ? slot - p.M : slot;
-      const uint32_t off =
-          r < len && lane_ok ? slot * (dh * (uint32_t)sizeof(float)) + c * 16 : 0x80000000u;
+      const uint32_t off = row_off(r0 + j * NG + g);
       kk[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, kNt));
       vv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, kNt));
     }
   };
-  // Online-softmax update with the 16 rows starting at r0.
-  auto consume_rows = [&](uint32_t r0, float4* kk, float4* vv) {
+  // The online-softmax update with the 16 rows starting at r0, in two halves.
+  // score_rows: the rows' scores from K, the running maximum and sum; leaves
+  // the weights of this lane's group's rows in pp and returns the factor the
+  // running sum of V rows is rescaled by.  accumulate_rows: that rescale and
+  // the weighted sum of the rows' V.
+  auto score_rows = [&](uint32_t r0, float4* kk, float* pp) {
     if (append && r0 == new_unit * RPI && g == new_g) {
 #pragma unroll
       for (int j = 0; j < RPG; ++j)
-        if (j == new_j) {
-          kk[j] = kn;
-          vv[j] = vn;
-        }
+        if (j == new_j) kk[j] = kn;
     }
     float s[RPG];
 #pragma unroll
@@ -237,7 +254,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float pp[RPG];
 #pragma unroll
     for (int j = 0; j < RPG; j += 4) {
       const float4 t = *reinterpret_cast<const float4*>(&s_p[wave][g * RPG + j]);
@@ -245,6 +261,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       pp[j + 1] = t.y;
       pp[j + 2] = t.z;
       pp[j + 3] = t.w;
+    }
+    return alpha;
+  };
+  auto accumulate_rows = [&](uint32_t r0, float4* vv, const float* pp, float alpha) {
+    if (append && r0 == new_unit * RPI && g == new_g) {
+#pragma unroll
+      for (int j = 0; j < RPG; ++j)
+        if (j == new_j) vv[j] = vn;
     }
     acc.x *= alpha;
     acc.y *= alpha;
@@ -288,20 +312,43 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       }
     }
   };
-  // One batch of 16 rows in flight per wave (16 KB, 64 KB per CU): loads,
-  // then the online-softmax update.  Deeper register pipelines (2-4 batches)
-  // lowered the HBM rate through the extra outstanding requests (32 heads x
-  // 128, 3000 rows: 19.4 us per launch with one batch, 20.4-21.1 us with 2-4).
+  // At most one unit of 16 rows in flight per wave (16 KB, 64 KB per CU):
+  // deeper register pipelines (2-4 units) lowered the HBM rate through the
+  // extra outstanding requests (32 heads x 128, 3000 rows: 19.4 us per launch
+  // with one unit, 20.4-21.1 us with 2-4).
   const uint32_t ustep = nsplit * WAVES;
   uint32_t u = split + nsplit * wave;
   float4 kk[RPG], vv[RPG];
-  if constexpr (WAVES > 1) store_new_row();
-  if (u < nunits) load_rows(u * RPI, kk, vv);
-  if constexpr (WAVES == 1) store_new_row();
-  while (u < nunits) {
-    consume_rows(u * RPI, kk, vv);
-    u += ustep;
+  float pp[RPG];
+  if constexpr (WAVES > 1) {
+    // Within that: the next unit's K rows are requested as soon as this
+    // unit's scores are formed and its V rows once the weighted sum has used
+    // this unit's, so the wave is never without loads in flight while it
+    // computes (19.51 vs 19.69 us per config-2 fused launch).  Rows past the
+    // window read zeros, so these loads need no condition.
+    store_new_row();
+    load_k(u * RPI, kk);
+    // Every K load ahead of every V load: a wait for K never waits for V.
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(u * RPI, vv);
+    while (u < nunits) {
+      const uint32_t r0 = u * RPI;
+      const uint32_t un = u + ustep;
+      const float alpha = score_rows(r0, kk, pp);
+      load_k(un * RPI, kk);
+      accumulate_rows(r0, vv, pp, alpha);
+      load_v(un * RPI, vv);
+      u = un;
+    }
+  } else {
     if (u < nunits) load_rows(u * RPI, kk, vv);
+    store_new_row();
+    while (u < nunits) {
+      const float alpha = score_rows(u * RPI, kk, pp);
+      accumulate_rows(u * RPI, vv, pp, alpha);
+      u += ustep;
+      if (u < nunits) load_rows(u * RPI, kk, vv);
+    }
   }
 
   // Merge the NG row groups of the wave (lanes c, c+G, ... hold the same dims).
