@@ -35,6 +35,8 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr int kGemmBufferWord3 = 0x00020000;  // raw 32-bit buffer, no swizzle
+
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
@@ -46,13 +48,17 @@ struct WTile {
 };
 
 // MAXT: the largest workgroup (64 * K/256 threads) the instance runs with;
-// 256 (K <= 1024) leaves the register file to the prefetch buffers.
+// 256 (K <= 1024) leaves the register file to the prefetch buffers.  Three
+// waves per SIMD (three 4-wave workgroups per CU at K <= 1024): one register
+// past 168 would leave room for two.
 template <bool SWIGLU, int MAXT>
-__global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(3)))
+void q4k_gemm_kernel(const Q4kGemmParams p) {
 #pragma clang fp contract(off)
   constexpr int NH = SWIGLU ? 2 : 1;
   __shared__ float part[16][NH][256];
   __shared__ float ssq[16][16];
+  __shared__ float s_inv[16];  // 1/rms of the tile's rows (RMSNorm)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int kb = tid >> 6;
@@ -84,8 +90,17 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
   load_w(cur, blockIdx.x);
 
   // x values of this lane: X[m][256 kb + 64 g + j], j < 64 (zero past M).
-  const uint32_t m = mt * 16 + r;
-  const bool m_ok = m < p.M;
+  // The tile's rows come in through a buffer resource that ends with its last
+  // row inside M, so rows past M read zeros: no per-row branch or select.
+  const uint32_t rows_here = min(16u, p.M - mt * 16);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(X) + (size_t)mt * 16 * p.ldx, 0,
+      (int)(((uint64_t)(rows_here - 1) * p.ldx + p.K) * sizeof(float)), kGemmBufferWord3);
+  auto ldx4 = [&](uint32_t row, uint32_t col) {
+    return __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(
+                    xrs, (uint32_t)((row * p.ldx + col) * sizeof(float)), 0, 0));
+  };
   float xv[64];
   if constexpr (MAXT <= 256) {
     // Through a per-wave LDS chunk (16 rows x 64 floats, pitch 68) so the
@@ -97,13 +112,8 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t mm = mt * 16 + 4 * i + (lane >> 4);
-        const float4 t = *(reinterpret_cast<const float4*>(
-                               X + (size_t)(mm < p.M ? mm : 0) * p.ldx + 256 * kb + 64 * c) +
-                           (lane & 15));
-        ld[c][i] = mm < p.M ? t : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int i = 0; i < 4; ++i)
+        ld[c][i] = ldx4(4 * i + (lane >> 4), 256 * kb + 64 * c + 4 * (lane & 15));
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -128,38 +138,41 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
     }
   } else {
     // Wide workgroups (K > 1024) read their rows directly.
-    const float4* xr =
-        reinterpret_cast<const float4*>(X + (size_t)(m_ok ? m : 0) * p.ldx + 256 * kb + 64 * g);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float4 t = xr[j];
-      xv[4 * j] = m_ok ? t.x : 0.f;
-      xv[4 * j + 1] = m_ok ? t.y : 0.f;
-      xv[4 * j + 2] = m_ok ? t.z : 0.f;
-      xv[4 * j + 3] = m_ok ? t.w : 0.f;
+      const float4 t = ldx4(r, 256 * kb + 64 * g + 4 * j);
+      xv[4 * j] = t.x;
+      xv[4 * j + 1] = t.y;
+      xv[4 * j + 2] = t.z;
+      xv[4 * j + 3] = t.w;
     }
   }
   if (p.norm_alpha) {
-    // RMSNorm of the 16 rows (shader_rmsnorm.wgsl:80-90): x * (1/rms) * alpha,
-    // with the sum of squares taken over this workgroup's registers.
+    // RMSNorm of the 16 rows (shader_rmsnorm.wgsl:80-90), x * (1/rms) * alpha,
+    // with the sum of squares taken over this workgroup's registers.  alpha
+    // scales x here and 1/rms (one factor per row) scales the row's outputs
+    // in the epilogue: sum_k w (x alpha) / rms, one multiply per x value
+    // instead of two.
     float q = 0.f;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) q += xv[j] * xv[j];
+    for (int j = 0; j < 64; ++j) q = __builtin_fmaf(xv[j], xv[j], q);
     q += __shfl_xor(q, 16, 64);
     q += __shfl_xor(q, 32, 64);
     if (g == 0) ssq[kb][r] = q;
     __syncthreads();
-    float tot = ssq[0][r];
-    for (uint32_t w = 1; w < KB; ++w) tot += ssq[w][r];
-    const float inv = 1.0f / sqrtf(tot / (float)p.K + p.norm_eps);
+    if (tid < 16) {
+      float tot = ssq[0][tid];
+      for (uint32_t w = 1; w < KB; ++w) tot += ssq[w][tid];
+      s_inv[tid] = 1.0f / sqrtf(tot / (float)p.K + p.norm_eps);
+    }
     const float4* al = reinterpret_cast<const float4*>(p.norm_alpha + 256 * kb + 64 * g);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float4 a = al[j];
-      xv[4 * j] = xv[4 * j] * inv * a.x;
-      xv[4 * j + 1] = xv[4 * j + 1] * inv * a.y;
-      xv[4 * j + 2] = xv[4 * j + 2] * inv * a.z;
-      xv[4 * j + 3] = xv[4 * j + 3] * inv * a.w;
+      xv[4 * j] = xv[4 * j] * a.x;
+      xv[4 * j + 1] = xv[4 * j + 1] * a.y;
+      xv[4 * j + 2] = xv[4 * j + 2] * a.z;
+      xv[4 * j + 3] = xv[4 * j + 3] * a.w;
     }
   }
 
@@ -174,6 +187,10 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
       uint32_t scl, mnl, sch, mnh;
       scale_min(hd.y, hd.z, hd.w, 2 * g, scl, mnl);
       scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sch, mnh);
+      // d1 = d*scale and m1 = dmin*min are exact in f32 (11-bit f16
+      // significands times 6-bit integers), and so is q*d1 (4-bit q), so
+      // fma(q, d1, -m1) rounds once, where the shader's (d*scale)*q - dmin*min
+      // rounds: the same weight, bit for bit.
       const float d1 = d * (float)scl, m1 = dmin * (float)mnl;
       const float d2 = d * (float)sch, m2 = dmin * (float)mnh;
       const uint32_t words[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
@@ -188,12 +205,12 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
         asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const float wl = (float)((lo >> (8 * b)) & 0xFFu) * d1 - m1;
+          const float wl = __builtin_fmaf((float)((lo >> (8 * b)) & 0xFFu), d1, -m1);
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(wl, xv[4 * w + b], acc[b], 0, 0, 0);
         }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const float wh = (float)((hi >> (8 * b)) & 0xFFu) * d2 - m2;
+          const float wh = __builtin_fmaf((float)((hi >> (8 * b)) & 0xFFu), d2, -m2);
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(wh, xv[32 + 4 * w + b], acc[b], 0, 0, 0);
         }
       }
@@ -207,9 +224,12 @@ __global__ __launch_bounds__(MAXT) void q4k_gemm_kernel(const Q4kGemmParams p) {
       const uint32_t mo = mt * 16 + (o & 15), no = t * 16 + (o >> 4);
       float v = part[0][0][o];
       for (uint32_t w = 1; w < KB; ++w) v += part[w][0][o];
+      const float inv = p.norm_alpha ? s_inv[o & 15] : 1.0f;
+      v *= inv;
       if constexpr (SWIGLU) {
         float u = part[0][NH - 1][o];
         for (uint32_t w = 1; w < KB; ++w) u += part[w][NH - 1][o];
+        u *= inv;
         v = v / (1.0f + expf(-v)) * u;
       }
       if (mo < p.M && no < nout) {
@@ -853,6 +873,10 @@ int launch_q4k_gemm(const Q4kGemmParams& p, hipStream_t stream) {
     return fail(STS_ERR_INVALID, "SwiGLU GEMM needs N = 2F (N=%u F=%u)", p.N, p.swiglu_f);
   if (p.ldx % 4 != 0 || p.x_zstride % 4 != 0 || (reinterpret_cast<uintptr_t>(p.x) & 15))
     return fail(STS_ERR_INVALID, "GEMM x rows must be 16-byte aligned");
+  // A 16-row tile of x is addressed through one buffer resource (31-bit range).
+  if ((uint64_t)p.ldx * 15 * sizeof(float) + (uint64_t)p.K * sizeof(float) > 0x7FFFFFF0ull)
+    return fail(STS_ERR_INVALID, "GEMM x row stride %llu too large",
+                (unsigned long long)p.ldx);
   for (uint32_t z = 0; z < p.Z; ++z)
     if (!p.w[z] || (reinterpret_cast<uintptr_t>(p.w[z]) & 15))
       return fail(STS_ERR_INVALID, "GEMM weights %u null or not 16-byte aligned", z);

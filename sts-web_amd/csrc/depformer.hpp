@@ -26,9 +26,10 @@ struct Q4kGemmParams {
   uint64_t ldx = 0, ldy = 0, ldr = 0;  // row strides (floats)
   uint64_t x_zstride = 0, y_zstride = 0;
   uint32_t swiglu_f = 0;
-  // With norm_alpha set, each x row is RMS-normalised on load:
-  // x * (1 / sqrt(sum x^2 / K + norm_eps)) * norm_alpha (shader_rmsnorm.wgsl's
-  // formula; the sum of squares is taken in this kernel's order).
+  // With norm_alpha set, each x row is RMS-normalised: x * (1 / sqrt(sum x^2 /
+  // K + norm_eps)) * norm_alpha (shader_rmsnorm.wgsl's formula), with the sum
+  // of squares taken in this kernel's order, alpha applied to x on load and
+  // the row's 1/rms to its outputs.
   const float* norm_alpha = nullptr;
   float norm_eps = 0.f;
   // Super-blocks per weight row when the launch covers only part of K (a
