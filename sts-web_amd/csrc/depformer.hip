@@ -102,49 +102,46 @@ void q4k_gemm_kernel(const Q4kGemmParams p) {
                     xrs, (uint32_t)((row * p.ldx + col) * sizeof(float)), 0, 0));
   };
   float xv[64];
-  if constexpr (MAXT <= 256) {
+  {
     // Through a per-wave LDS chunk (16 rows x 64 floats, pitch 68) so the
     // global loads are coalesced: instruction i of chunk c reads rows
     // 4i..4i+3, 256 contiguous bytes each; the lanes of slot g then copy
-    // chunk g (the 16 lanes of a read phase hit distinct banks).
+    // chunk g (the 16 lanes of a read phase hit distinct banks).  (Each lane
+    // reading its own 256 bytes would touch 64 cache lines per instruction.)
+    // Chunks in flight at once: all four where a wave may hold 168 registers,
+    // two in the 16-wave instance (128).
+    constexpr int CIF = MAXT <= 256 ? 4 : 2;
     __shared__ __align__(16) float xs[MAXT / 64][16][68];
-    float4 ld[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c0 = 0; c0 < 4; c0 += CIF) {
+      float4 ld[CIF][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ld[c][i] = ldx4(4 * i + (lane >> 4), 256 * kb + 64 * c + 4 * (lane & 15));
+      for (int c = 0; c < CIF; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+        for (int i = 0; i < 4; ++i)
+          ld[c][i] = ldx4(4 * i + (lane >> 4), 256 * kb + 64 * (c0 + c) + 4 * (lane & 15));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<float4*>(&xs[kb][4 * i + (lane >> 4)][4 * (lane & 15)]) = ld[c][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (g == c) {
+      for (int c = 0; c < CIF; ++c) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float4 t = *reinterpret_cast<const float4*>(&xs[kb][r][4 * j]);
-          xv[4 * j] = t.x;
-          xv[4 * j + 1] = t.y;
-          xv[4 * j + 2] = t.z;
-          xv[4 * j + 3] = t.w;
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4*>(&xs[kb][4 * i + (lane >> 4)][4 * (lane & 15)]) = ld[c][i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (g == c0 + c) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const float4 t = *reinterpret_cast<const float4*>(&xs[kb][r][4 * j]);
+            xv[4 * j] = t.x;
+            xv[4 * j + 1] = t.y;
+            xv[4 * j + 2] = t.z;
+            xv[4 * j + 3] = t.w;
+          }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-  } else {
-    // Wide workgroups (K > 1024) read their rows directly.
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float4 t = ldx4(r, 256 * kb + 64 * g + 4 * j);
-      xv[4 * j] = t.x;
-      xv[4 * j + 1] = t.y;
-      xv[4 * j + 2] = t.z;
-      xv[4 * j + 3] = t.w;
     }
   }
   if (p.norm_alpha) {
