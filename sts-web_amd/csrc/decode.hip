@@ -146,9 +146,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   const uint32_t nunits = (len + RPI - 1) / RPI;
 
   const size_t qoff = b * p.q_bstride + (size_t)h * dh + c * 4;
-  // q is rotated and scaled before the first K/V loads are issued: issuing
-  // them first and waiting for q afterwards measured ~1 us slower per
-  // config-2 launch (20.3 vs 19.25 us), on the same box.
+  // The 4-wave kernel rotates and scales q before its first K/V loads are
+  // issued: issuing them first and waiting for q afterwards measured ~1 us
+  // slower per config-2 launch (20.3 vs 19.25 us), the chip-wide burst of K/V
+  // requests delaying every wave's q.  The one-wave kernel (a few rows per
+  // wave) issues its K/V loads first, so the two round trips overlap.
   float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f);
   if (lane_ok) q4 = ld4(p.q + qoff);
   float2 rc = make_float2(0.f, 0.f), rs = make_float2(0.f, 0.f);
@@ -158,12 +160,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     const size_t ro = (size_t)pos * (dh / 2) + c * 2;
     rc = *reinterpret_cast<const float2*>(p.rope_cos + ro);
     rs = *reinterpret_cast<const float2*>(p.rope_sin + ro);
-    q4 = rope4(q4, rc, rs);
   }
-  q4.x *= p.scale_log2;
-  q4.y *= p.scale_log2;
-  q4.z *= p.scale_log2;
-  q4.w *= p.scale_log2;
+  auto prep_q = [&]() {
+    if (rope) q4 = rope4(q4, rc, rs);
+    q4.x *= p.scale_log2;
+    q4.y *= p.scale_log2;
+    q4.z *= p.scale_log2;
+    q4.w *= p.scale_log2;
+  };
+  if constexpr (WAVES > 1) prep_q();
 
   // The K/V head of this query head (no division on the common group-1 path).
   const uint32_t kvh = p.group == 1 ? h : h / p.group;
@@ -341,7 +346,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
       u = un;
     }
   } else {
-    if (u < nunits) load_rows(u * RPI, kk, vv);
+    // u = 0 < nunits here (the window is not empty); no condition, so the
+    // wait for q below does not wait for these loads.
+    load_rows(u * RPI, kk, vv);
+    prep_q();
     store_new_row();
     while (u < nunits) {
       const float alpha = score_rows(u * RPI, kk, pp);
