@@ -467,6 +467,7 @@ int sts_rmsnorm(const float* x, const float* alpha, float* out, uint32_t rows, u
  * h[b][e] = proj[b][e] + E[token_b][e] for a Q4_0 embedding table E [vocab][dim]
  * (wgsl/shader_embed_q4.wgsl + shader_vec_add.wgsl, depth_engine.rs:988-1057);
  * token_b = tokens[b * tok_stride] (device), out-of-vocab tokens embed as zeros.
+ * The table is 2-byte aligned (each 18-byte block starts with its f16 scale).
  */
 int sts_embed_add_q4_0(const uint8_t* table, uint32_t vocab, const uint32_t* tokens,
                        uint64_t tok_stride, const float* proj, float* h, uint32_t batch,

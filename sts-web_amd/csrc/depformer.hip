@@ -274,18 +274,22 @@ __global__ __launch_bounds__(256) void embed_add_kernel(const uint8_t* __restric
   const uint32_t e = blockIdx.x * 256 + threadIdx.x;
   const uint32_t b = blockIdx.y;
   if (e >= D) return;
+  // Two memory round trips: the projection with the token, then the three
+  // bytes of the token's Q4_0 block this element needs, all at once (an
+  // out-of-range token reads row 0 and adds nothing).
+  const float pv = proj[(size_t)b * D + e];
   const uint32_t tok = tokens[(size_t)b * tok_stride];
-  float emb = 0.f;
-  if (tok < vocab) {
-    const uint8_t* blk = table + ((size_t)tok * (D / 32) + e / 32) * 18;
-    const uint32_t bits = blk[0] | ((uint32_t)blk[1] << 8);
-    // An Inf/NaN scale reads as 0 (shader_embed_q4.wgsl:48-51).
-    const float scale = ((bits >> 10) & 0x1Fu) == 0x1Fu ? 0.f : half_bits_to_float(bits);
-    const uint32_t pos = e % 32;
-    const uint32_t nib = pos < 16 ? (blk[2 + pos] & 0xFu) : (blk[2 + pos - 16] >> 4);
-    emb = ((float)nib - 8.0f) * scale;
-  }
-  h[(size_t)b * D + e] = proj[(size_t)b * D + e] + emb;
+  const bool ok = tok < vocab;
+  const uint8_t* blk = table + ((size_t)(ok ? tok : 0u) * (D / 32) + e / 32) * 18;
+  const uint32_t pos = e % 32;
+  // The f16 scale as one 16-bit load (18-byte blocks keep it 2-byte aligned).
+  const uint32_t bits = *reinterpret_cast<const uint16_t*>(blk);
+  const uint32_t qb = blk[2 + (pos & 15u)];
+  // An Inf/NaN scale reads as 0 (shader_embed_q4.wgsl:48-51).
+  const float scale = ((bits >> 10) & 0x1Fu) == 0x1Fu ? 0.f : half_bits_to_float(bits);
+  const uint32_t nib = pos < 16 ? (qb & 0xFu) : (qb >> 4);
+  const float emb = ok ? ((float)nib - 8.0f) * scale : 0.f;
+  h[(size_t)b * D + e] = pv + emb;
 }
 
 // Monotone map of a float to a uint32 (larger float -> larger key), and back.
@@ -943,6 +947,8 @@ int launch_embed_add(const uint8_t* table, uint32_t vocab, const uint32_t* token
                      hipStream_t stream) {
   if (D % 32 != 0 || B == 0 || B > 65535u)
     return fail(STS_ERR_INVALID, "embedding: dim %u must be a multiple of 32, batch %u", D, B);
+  if (reinterpret_cast<uintptr_t>(table) & 1)
+    return fail(STS_ERR_INVALID, "embedding table must be 2-byte aligned (its f16 scales)");
   hipLaunchKernelGGL(embed_add_kernel, dim3((D + 255) / 256, B), dim3(256), 0, stream, table,
                      vocab, tokens, tok_stride, proj, h, D);
   STS_HIP(hipGetLastError());

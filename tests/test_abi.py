@@ -310,6 +310,8 @@ def test_depformer_chain_argument_errors():
     assert "eps" in _err(lib.sts_rmsnorm(FAKE, FAKE, FAKE, 4, 1024, float("nan"), None))
     assert "multiple of 32" in _err(lib.sts_embed_add_q4_0(FAKE, 10, FAKE, 1, FAKE, FAKE, 2, 100,
                                                           None))
+    assert "aligned" in _err(lib.sts_embed_add_q4_0(FAKE + 1, 10, FAKE, 1, FAKE, FAKE, 2, 128,
+                                                   None))
     assert "vocab" in _err(lib.sts_sample_topk(FAKE, 5000, 2, 5000, 10, 1.0, 1.0, FAKE, FAKE, 30,
                                                FAKE, 1, FAKE, 1, None))
     assert "top_k" in _err(lib.sts_sample_topk(FAKE, 2048, 2, 2048, 257, 1.0, 1.0, FAKE, FAKE, 30,
