@@ -448,6 +448,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   ticket = __builtin_amdgcn_readfirstlane(ticket);
   if (ticket != nsplit - 1) return;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Every other split of (b, h) has taken its ticket: the counter is reset
+  // now, its round trip overlapping the merge's loads.
+  if (lane == 0) atomicExch(ctr, 0u);
 
   // Merge: lane s < nsplit fetches split s's (m, l); lane (grp, col) fetches
   // column col of the splits grp, grp + NG2, ... in passes of kPass records,
@@ -508,7 +511,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   o4.w += xor32(o4.w);
   if (lane < C4 && (!PAD || (uint32_t)col * 4 < dh))
     st4(outp + col * 4, make_float4(o4.x / l, o4.y / l, o4.z / l, o4.w / l));
-  if (lane == 0) atomicExch(ctr, 0u);
 }
 
 }  // namespace

@@ -446,6 +446,9 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
   __syncthreads();
   if (s_ticket != ns - 1) return;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  // Every other split has taken its ticket: reset the counter now, its round
+  // trip overlapping the loads of the fold.
+  if (tid == 0) atomicExch(ctr, 0u);
 
   // Last to arrive: fold the splits in split order (whichever arrived last),
   // so the result does not depend on arrival order.
@@ -502,7 +505,6 @@ __global__ __launch_bounds__(256 * KSPLIT) void prefill_kernel(const PrefillPara
       }
     }
   }
-  if (tid == 0) atomicExch(ctr, 0u);
 }
 
 // ---------------------------------------------------------------------------
