@@ -436,10 +436,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   const __amdgpu_buffer_rsrc_t part_rs = coherent_rsrc(p.part + rec_base, p.nsplit_max * REC * 4);
   const uint32_t rec = split * REC * 4;  // byte offset of this split's record
   if (lane < C4) st_coherent4(part_rs, rec + col * 16, coh_f4{a4.x, a4.y, a4.z, a4.w});
-  if (lane == 0) {
-    st_coherent(part_rs, rec + D * 4, m_t);
-    st_coherent(part_rs, rec + D * 4 + 4, l_t);
-  }
+  // (m, l) and the record's two pad words as one 16-byte store: whole
+  // segments written through, like the rows above.
+  if (lane == 0) st_coherent4(part_rs, rec + D * 4, coh_f4{m_t, l_t, 0.f, 0.f});
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   uint32_t* ctr = p.counters + (size_t)b * p.H + h;
@@ -458,8 +457,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   constexpr int kPass = 4;
   float ms = -FLT_MAX, ls = 0.f;
   if (lane < (int)nsplit) {
-    ms = ld_coherent(part_rs, (lane * REC + D) * 4);
-    ls = ld_coherent(part_rs, (lane * REC + D + 1) * 4);
+    const coh_f4 ml = ld_coherent4(part_rs, (lane * REC + D) * 4);
+    ms = ml.x;
+    ls = ml.y;
   }
   float4 raw[kPass];
   auto fetch = [&](uint32_t s0) {
