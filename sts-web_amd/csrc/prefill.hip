@@ -48,6 +48,7 @@ namespace sts {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -593,9 +594,6 @@ __device__ __forceinline__ void ws_signal(uint32_t* ctr, int lane) {
 template <int D, bool SPLIT, bool KV16 = false>
 __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) {
   static_assert(!(SPLIT && KV16), "the split variant needs the f32 rows");
-  // Consumers one block ahead where the registers allow it (the bf16-input
-  // producers hold half the bytes of the f32-input ones).
-  constexpr bool PIPE = KV16;
   using Stage = WsStage<D, SPLIT>;
   constexpr int KB = kWsKB;
   constexpr int NS = SPLIT ? 2 : kWsStages;
@@ -1016,13 +1014,18 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         qop[0][a] = *reinterpret_cast<const bf16x8*>(&qs[(qg * 32 + l32) * QP + a * 16 + hh * 8]);
     }
     // Scores S^T of block i: waits for its stage, K operands from LDS, MFMAs.
-    auto s_block = [&](uint32_t i) {
+    // The scores accumulate onto -mb, mb the running maximum when they are
+    // issued (0 before the first block), so they come out of the MFMAs
+    // relative to it: the softmax subtracts nothing unless the base has
+    // moved since (the first block, a lazy rescale).
+    auto base_of = [&]() { return m == -FLT_MAX ? 0.f : m; };
+    auto s_block = [&](uint32_t i, float mb) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane, p.err);
       const Stage& sg = st[s];
       f32x16 sc;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+      for (int v = 0; v < 16; ++v) sc[v] = -mb;
 #pragma unroll
       for (int pl = 0; pl < QPL; ++pl) {
         // K plane pl against Q hi, and (SPLIT, K hi only) against Q lo.
@@ -1042,7 +1045,7 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       return sc;
     };
     // Mask, online softmax and O^T += V^T P^T of block i; releases its stage.
-    auto finish_block = [&](uint32_t i, f32x16 sc) {
+    auto finish_block = [&](uint32_t i, f32x16 sc, float mb) {
       const uint32_t s = i % NS;
       const Stage& sg = st[s];
       const uint32_t k0 = blk(i) * KB + ks * 32;
@@ -1054,10 +1057,11 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
           sc[v] = (key <= w_q && key < kend) ? sc[v] : -INFINITY;
         }
       }
+      // sc holds the scores less mb; the block maximum is mx + mb.
       float mx = sc[0];
 #pragma unroll
       for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[v]);
-      mx = max_xor32(mx);
+      mx = max_xor32(mx) + mb;
       // Lazy rescaling: the weights stay relative to the base m until some
       // query's block maximum exceeds it by more than kLazyLog2 (weights then
       // stay <= 2^kLazyLog2); only then does the base move and O get
@@ -1070,14 +1074,20 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
 #pragma unroll
         for (int t = 0; t < OT; ++t) o[t] *= alpha;
       }
+      // The weights exp2(s - m): sc already less mb, so only a moved base
+      // needs a subtraction.
+      const float dm = m - mb;
+      if (__any(dm != 0.f)) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[v] -= dm;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float e = fast_exp2(sc[v] - m);
+        const float e = fast_exp2(sc[v]);
         sc[v] = e;
-        ps += e;
+        if constexpr (SPLIT) ps += e;
       }
-      lsum += sum_xor32(ps);
       bf16x8 pb[QPL][2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -1087,6 +1097,19 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
           pb[0][c][j] = hi;
           if constexpr (SPLIT) pb[QPL - 1][c][j] = bf16_lo(sc[8 * c + j], hi);
         }
+      if constexpr (!SPLIT) {
+        // The row sum of the weights as the products will use them, rounded
+        // to bf16: two bf16 weights per v_dot2 with (1, 1), f32 accumulate.
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        float ps1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          ps = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[0][0][j], pb[0][0][j + 1]}, ones, ps, false);
+          ps1 = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[0][1][j], pb[0][1][j + 1]}, ones, ps1, false);
+        }
+        ps += ps1;
+      }
+      lsum += sum_xor32(ps);
       // V^T operands are read per output tile after the softmax (the stage
       // stays claimed until they are in registers), then the stage is released.
       if constexpr (SPLIT) ws_wait_ge(&vfilled[s], 4 * (i / NS + 1), p.wait_limit, lane, p.err);
@@ -1112,19 +1135,12 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
       }
       ws_signal(&released[s], lane);
     };
-    if constexpr (PIPE) {
-      // One block ahead: the next block's score MFMAs are issued before this
-      // block's softmax, so the matrix pipe works while the VALU does the
-      // softmax (the consumers hold two stages at a time).
-      f32x16 sc = s_block(0);
-      for (uint32_t i = 0; i < nblk; ++i) {
-        f32x16 sn = sc;
-        if (i + 1 < nblk) sn = s_block(i + 1);
-        finish_block(i, sc);
-        sc = sn;
-      }
-    } else {
-      for (uint32_t i = 0; i < nblk; ++i) finish_block(i, s_block(i));
+    // (Consumers one block ahead, the next block's score MFMAs issued before
+    // this block's softmax, measured slower once the softmax lost the
+    // subtraction and the row-sum additions: mirror 16.9 against 16.1 us.)
+    for (uint32_t i = 0; i < nblk; ++i) {
+      const float mb = base_of();
+      finish_block(i, s_block(i, mb), mb);
     }
   }
 
