@@ -1018,14 +1018,17 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // issued (0 before the first block), so they come out of the MFMAs
     // relative to it: the softmax subtracts nothing unless the base has
     // moved since (the first block, a lazy rescale).
-    auto base_of = [&]() { return m == -FLT_MAX ? 0.f : m; };
-    auto s_block = [&](uint32_t i, float mb) {
+    // The base's negation is kept in a tile of its own, the first MFMA's
+    // accumulator input, and rewritten only when the base moves.
+    float mbase = 0.f;
+    f32x16 nbase;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) nbase[v] = -0.f;
+    auto s_block = [&](uint32_t i) {
       const uint32_t s = i % NS, use = i / NS;
       ws_wait_ge(&filled[s], 4 * (use + 1), p.wait_limit, lane, p.err);
       const Stage& sg = st[s];
-      f32x16 sc;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sc[v] = -mb;
+      f32x16 sc = nbase;
 #pragma unroll
       for (int pl = 0; pl < QPL; ++pl) {
         // K plane pl against Q hi, and (SPLIT, K hi only) against Q lo.
@@ -1073,6 +1076,9 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
         lsum *= alpha;
 #pragma unroll
         for (int t = 0; t < OT; ++t) o[t] *= alpha;
+        mbase = m == -FLT_MAX ? 0.f : m;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) nbase[v] = -mbase;
       }
       // The weights exp2(s - m): sc already less mb, so only a moved base
       // needs a subtraction.
@@ -1139,8 +1145,8 @@ __global__ __launch_bounds__(512) void prefill_ws_kernel(const PrefillParams p) 
     // this block's softmax, measured slower once the softmax lost the
     // subtraction and the row-sum additions: mirror 16.9 against 16.1 us.)
     for (uint32_t i = 0; i < nblk; ++i) {
-      const float mb = base_of();
-      finish_block(i, s_block(i, mb), mb);
+      const float mb = mbase;
+      finish_block(i, s_block(i), mb);
     }
   }
 
