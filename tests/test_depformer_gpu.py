@@ -339,6 +339,31 @@ def test_depformer_chain_small(gpu):
     eng.close()
 
 
+def test_depformer_chain_tied_logits(gpu):
+    """Output rows duplicated in pairs, so every logit has an equal twin and
+    each draw is decided by the replay of the shader's selection; the next
+    step's input (the drawn token's embedding, added by the sampler) must
+    still follow the oracle chain."""
+    w = oracle.DepformerWeights.synthetic(CFG, seed=5)
+    V = CFG["out_vocab"]
+    for s, ol in enumerate(w.output_linear):
+        a = np.array(ol).reshape(V, -1)
+        a[1::2] = a[0::2]
+        w.output_linear[s] = a.reshape(np.shape(ol))
+    B = 4
+    th, text, rand, pt, npn = _inputs(CFG, B, 23)
+    eng = sts_attn.DepthEngine(_config(CFG), _device_weights(w), max_batch=B)
+    logits = torch.empty((CFG["num_steps"], B, V), device="cuda")
+    tokens = eng.generate(dev(th), dev(text.view(np.int32)), 0.8, 20, 1.2, dev(rand),
+                          dev(pt.view(np.int32)), dev(npn.view(np.int32)), logits=logits)
+    lg = host(logits)
+    assert np.array_equal(lg[:, :, 0::2], lg[:, :, 1::2])
+    n = _check_streams(CFG, w, th, text, rand, pt, npn, host(tokens).view(np.uint32), lg, 20,
+                       0.8, 1.2, range(B))
+    assert n >= B * CFG["num_steps"] - 2
+    eng.close()
+
+
 def test_depformer_chain_golden_fixture(gpu):
     """tests/golden/depformer_chain_small.npz: the GPU chain's tokens equal
     the fixture's and its logits are within 1e-4 of their scale."""
