@@ -474,6 +474,51 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     }
   };
   fetch(0);
+  if (nsplit <= (uint32_t)(NG2 * kPass)) {
+    // One pass: the splits' (m, l) broadcast from their lanes as uniform
+    // values, so the weights need no exchange between lanes.
+    constexpr int NSX = NG2 * kPass;
+    float mu[NSX], lu[NSX];
+#pragma unroll
+    for (int t = 0; t < NSX; ++t) {
+      mu[t] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ms), t));
+      lu[t] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), t));
+    }
+    float mg = mu[0];
+#pragma unroll
+    for (int t = 1; t < NSX; ++t) mg = fmaxf(mg, mu[t]);
+    float fl[NSX];
+    float l = 0.f;
+#pragma unroll
+    for (int t = 0; t < NSX; ++t) {
+      fl[t] = fast_exp2(mu[t] - mg);  // 0 for the lanes past nsplit (m = -FLT_MAX)
+      l += fl[t] * lu[t];
+    }
+    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kPass; ++i) {
+      float f = fl[NG2 * i];
+#pragma unroll
+      for (int g = 1; g < NG2; ++g) f = grp == g ? fl[g + NG2 * i] : f;
+      o4.x += f * raw[i].x;
+      o4.y += f * raw[i].y;
+      o4.z += f * raw[i].z;
+      o4.w += f * raw[i].w;
+    }
+    if constexpr (NG2 == 4) {
+      o4.x += xchg<4>(o4.x);
+      o4.y += xchg<4>(o4.y);
+      o4.z += xchg<4>(o4.z);
+      o4.w += xchg<4>(o4.w);
+    }
+    o4.x += xor32(o4.x);
+    o4.y += xor32(o4.y);
+    o4.z += xor32(o4.z);
+    o4.w += xor32(o4.w);
+    if (lane < C4 && (!PAD || (uint32_t)col * 4 < dh))
+      st4(outp + col * 4, make_float4(o4.x / l, o4.y / l, o4.z / l, o4.w / l));
+    return;
+  }
   float mg = ms;
   mg = fmaxf(mg, xchg<0>(mg));
   mg = fmaxf(mg, xchg<1>(mg));
