@@ -108,8 +108,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
   static_assert(RPI == 16, "16 rows per wave iteration");
 
   __shared__ __align__(16) float s_p[WAVES][RPI];
-  __shared__ __align__(16) float s_acc[WAVES][D];
-  __shared__ float s_ml[WAVES][2];
+  __shared__ __align__(16) float s_acc[WAVES * NG][D];
+  __shared__ float s_ml[WAVES * NG][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -359,57 +359,41 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(const DecodeParams p
     }
   }
 
-  // Merge the NG row groups of the wave (lanes c, c+G, ... hold the same dims).
-  float mw = m;
-  if constexpr (NG == 4) mw = fmaxf(mw, xchg<4>(mw));
-  mw = fmaxf(mw, xor32(mw));
-  {
-    const float f = fast_exp2(m - mw);
-    acc.x *= f;
-    acc.y *= f;
-    acc.z *= f;
-    acc.w *= f;
-    lsum *= f;
-  }
-  if constexpr (NG == 4) {
-    acc.x += xchg<4>(acc.x);
-    acc.y += xchg<4>(acc.y);
-    acc.z += xchg<4>(acc.z);
-    acc.w += xchg<4>(acc.w);
-  }
-  acc.x += xor32(acc.x);
-  acc.y += xor32(acc.y);
-  acc.z += xor32(acc.z);
-  acc.w += xor32(acc.w);
-  // Each row's weight sits in the 4 lanes of a quad: the 64-lane sum is 4x.
-  const float lw = wave_sum(lsum) * 0.25f;
+  // Each row's weight sits in the 4 lanes of a quad: the group's sum of
+  // weights is the sum over its quads.
+  float lg = lsum;
+  lg += xchg<2>(lg);
+  lg += xchg<3>(lg);
+  if constexpr (G == 32) lg += xchg<4>(lg);
 
-  // Merge the waves through LDS; wave 0 then finishes alone (no more
-  // workgroup barriers on the critical path): lane (grp, col) of wave 0
+  // The WAVES x NG row groups' states (acc, m, l) go to LDS as they are, and
+  // wave 0 merges them all at once (no exchanges between lanes before the
+  // barrier, no more workgroup barriers after it): lane (grp, col) of wave 0
   // handles the float4 column col = lane % C4 of the head.
   constexpr int C4 = D / 4;
   constexpr int NG2 = 64 / C4;  // lane groups per wave: 2 for D = 128, 4 for D = 64
-  if (lane < G) st4(&s_acc[wave][c * 4], acc);
-  if (lane == 0) {
-    s_ml[wave][0] = mw;
-    s_ml[wave][1] = lw;
+  constexpr int NST = WAVES * NG;
+  st4(&s_acc[wave * NG + g][c * 4], acc);
+  if (c == 0) {
+    s_ml[wave * NG + g][0] = m;
+    s_ml[wave * NG + g][1] = lg;
   }
   __syncthreads();
   if (wave != 0) return;
   float m_t = s_ml[0][0];
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) m_t = fmaxf(m_t, s_ml[w][0]);
-  float fw[WAVES];
+  for (int w = 1; w < NST; ++w) m_t = fmaxf(m_t, s_ml[w][0]);
+  float fw[NST];
   float l_t = 0.f;
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
+  for (int w = 0; w < NST; ++w) {
     fw[w] = fast_exp2(s_ml[w][0] - m_t);
     l_t += fw[w] * s_ml[w][1];
   }
   const int col = lane % C4, grp = lane / C4;
   float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) {
+  for (int w = 0; w < NST; ++w) {
     const float4 x = *reinterpret_cast<const float4*>(&s_acc[w][col * 4]);
     a4.x += fw[w] * x.x;
     a4.y += fw[w] * x.y;
